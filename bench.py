@@ -1,0 +1,344 @@
+#!/usr/bin/env python3
+"""Benchmark: HBM throughput of the Qwen3 decoder layer's non-GEMM chain on
+one MI355X (gfx950), through the C ABI of libq3k.so.
+
+A step is one pass of the per-layer non-GEMM chain over one batch of
+synthetic input at BASELINE config 4 (Qwen3-8B prefill, T = 8192 tokens as
+4 sequences x 2048, positions 0..2047 per sequence):
+
+  add_rms_norm  h1 += d1; y1 = rmsnorm(h1)     [8192, 4096]   attention residual + post-attention norm
+  qk_norm_rope  Q [8192, 32, 128], K [8192, 8, 128]           per-head norm + RoPE, in place
+  add_rms_norm  h2 += d2; y2 = rmsnorm(h2)     [8192, 4096]   MLP residual + next layer's input norm
+  silu_mul      o = silu(g) * u                [8192, 12288]
+
+Every tensor of a step is distinct and the steps rotate over two full input
+sets (2 x 1.31 GB, far above the 256 MB Infinity Cache), so each launch reads
+its inputs from HBM.  ``value`` is the chain's algorithmic bytes (each
+compulsory byte once) divided by the measured time per step, inputs already
+resident in HBM.  Per-kernel durations come from HIP events around every
+launch inside the same timed region.
+
+Also reported (not part of ``value``): the embedding gather and the final
+RMSNorm at config 4, the same chain built from the unfused drop-in ops in
+the reference's order, a 128-bit copy ceiling, and the CPU baseline (the
+oracle's restatement of the reference's CPU arithmetic, timed on this host).
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import importlib.util
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+PKG = "qwen3-runtime-byyourself_amd"
+METRIC = "HBM GB/s (% of peak) for RMSNorm/QK-norm+RoPE/SwiGLU at Qwen3-8B shapes"
+PEAK_GBS = 8000.0
+EPS = 1e-6
+D = 128
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c4")
+    ap.add_argument("--sets", type=int, default=2, help="rotating input sets")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extras", action="store_true", help="chain only (no embedding/final-norm/unfused/copy)")
+    return ap.parse_args()
+
+
+class Timer:
+    """Per-launch HIP event pairs recorded on the launch stream."""
+
+    def __init__(self, hip, stream, names, steps):
+        self.hip, self.stream = hip, stream
+        self.events = {n: [(hip.Event(), hip.Event()) for _ in range(steps)] for n in names}
+
+    def run(self, name, i, fn):
+        a, b = self.events[name][i]
+        a.record(self.stream)
+        fn()
+        b.record(self.stream)
+
+    def mean_ms(self, name):
+        return float(np.mean([a.elapsed_ms(b) for a, b in self.events[name]]))
+
+
+def make_chain_set(hip, synth, configs, c, q3k, seed_shift=0):
+    T, H, I = c.tokens, c.hidden, c.inter
+    s = c.seed
+    DB = hip.DeviceBuffer.from_array
+    bufs = {
+        "h1": DB(synth.normal_bf16(s, configs.TID_H, (T, H))),
+        "d1": DB(synth.normal_bf16(s, configs.TID_D1, (T, H))),
+        "w1": DB(synth.normal_bf16(s, configs.TID_W1, (H,), mean=1.0, std=0.1)),
+        "y1": hip.DeviceBuffer(T * H * 2),
+        "q": DB(synth.normal_bf16(s, configs.TID_Q, (T, c.heads_q * D))),
+        "k": DB(synth.normal_bf16(s, configs.TID_K, (T, c.heads_kv * D))),
+        "qw": DB(synth.normal_bf16(s, configs.TID_QW, (D,), mean=1.0, std=0.1)),
+        "kw": DB(synth.normal_bf16(s, configs.TID_KW, (D,), mean=1.0, std=0.1)),
+        "h2": DB(synth.normal_bf16(s, configs.TID_H2, (T, H))),
+        "d2": DB(synth.normal_bf16(s, configs.TID_D2, (T, H))),
+        "w2": DB(synth.normal_bf16(s, configs.TID_W2, (H,), mean=1.0, std=0.1)),
+        "y2": hip.DeviceBuffer(T * H * 2),
+        "g": DB(synth.normal_bf16(s, configs.TID_GATE, (T, I))),
+        "u": DB(synth.normal_bf16(s, configs.TID_UP, (T, I))),
+        "o": hip.DeviceBuffer(T * I * 2),
+        "cache": DB(q3k.build_rope_cache(c.max_pos, D, configs.THETA)),
+    }
+    return bufs
+
+
+def clone_set(hip, src):
+    out = {}
+    for k, b in src.items():
+        nb = hip.DeviceBuffer(b.nbytes)
+        nb.copy_from(b)
+        out[k] = nb
+    return out
+
+
+def chain_ops(q3k, c, b, stream):
+    T, H = c.tokens, c.hidden
+    return [
+        ("add_rms_norm_attn", lambda: q3k.add_rms_norm(b["h1"], b["d1"], b["w1"], b["y1"], T, H, EPS, stream)),
+        ("qk_norm_rope", lambda: q3k.qk_norm_rope(b["q"], b["k"], b["qw"], b["kw"], c.batch, c.seq, c.heads_q,
+                                                  c.heads_kv, D, EPS, b["cache"], c.max_pos, 0, None, stream)),
+        ("add_rms_norm_mlp", lambda: q3k.add_rms_norm(b["h2"], b["d2"], b["w2"], b["y2"], T, H, EPS, stream)),
+        ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * c.inter, stream)),
+    ]
+
+
+def unfused_ops(q3k, c, b, stream):
+    """The same chain through the drop-in ops in the reference's order
+    (decoder_layer.cpp:78->88, self_attention.cpp:147-152, mlp.cpp:111, :94->:72)."""
+    T, H = c.tokens, c.hidden
+    return [
+        ("add_inplace", lambda: q3k.add_inplace(b["h1"], b["d1"], T * H, stream)),
+        ("rms_norm", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream)),
+        ("rms_norm_q", lambda: q3k.rms_norm(b["q"], b["qw"], b["o"], T * c.heads_q, D, EPS, stream)),
+        ("rms_norm_k", lambda: q3k.rms_norm(b["k"], b["kw"], b["y2"], T * c.heads_kv, D, EPS, stream)),
+        ("rope_q", lambda: q3k.rope(b["o"], c.batch, c.seq, c.heads_q, D, b["cache"], c.max_pos, 0, None, stream)),
+        ("rope_k", lambda: q3k.rope(b["y2"], c.batch, c.seq, c.heads_kv, D, b["cache"], c.max_pos, 0, None, stream)),
+        ("add_inplace_2", lambda: q3k.add_inplace(b["h2"], b["d2"], T * H, stream)),
+        ("rms_norm_2", lambda: q3k.rms_norm(b["h2"], b["w2"], b["y2"], T, H, EPS, stream)),
+        ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * c.inter, stream)),
+    ]
+
+
+def time_ops(hip, stream, sets, make_ops, steps, warmup):
+    """Warm up, then time `steps` passes (rotating over `sets`) with per-op events.
+    Returns (ms per step, {op: mean ms})."""
+    names = [n for n, _ in make_ops(sets[0])]
+    per_set = [make_ops(s) for s in sets]
+    for i in range(warmup):
+        for _, fn in per_set[i % len(sets)]:
+            fn()
+    stream.synchronize()
+    timer = Timer(hip, stream, names, steps)
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        for n, fn in per_set[i % len(sets)]:
+            timer.run(n, i, fn)
+    stop.record(stream)
+    stop.synchronize()
+    hip.synchronize()
+    total = start.elapsed_ms(stop)
+    return total / steps, {n: timer.mean_ms(n) for n in names}
+
+
+def read_traffic(kernel_key):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    path = os.path.join(REPO, "profiles", "pmc_traffic_c4.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.strip().strip("|").split("|")
+            if len(parts) >= 2 and parts[0].strip() == kernel_key:
+                try:
+                    return int(float(parts[-1].strip()))
+                except ValueError:
+                    return None
+    return None
+
+
+def cpu_baseline(configs, synth, seconds):
+    """The oracle (a C restatement of the reference's CPU arithmetic) on a
+    bounded sample of the config-4 chain: the same four ops over the first
+    Ts tokens, repeated until `seconds` elapse, on all host cores and on one."""
+    spec = importlib.util.spec_from_file_location("q3k_oracle", os.path.join(REPO, "oracle", "q3k_oracle.py"))
+    oracle = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(oracle)
+    c = configs.CONFIGS["c4"]
+    Ts, H, I = 256, c.hidden, c.inter
+    h1 = synth.normal_bf16(c.seed, configs.TID_H, (Ts, H))
+    d1 = synth.normal_bf16(c.seed, configs.TID_D1, (Ts, H))
+    w1 = synth.normal_bf16(c.seed, configs.TID_W1, (H,), mean=1.0, std=0.1)
+    q = synth.normal_bf16(c.seed, configs.TID_Q, (1, Ts, c.heads_q * D))
+    k = synth.normal_bf16(c.seed, configs.TID_K, (1, Ts, c.heads_kv * D))
+    qw = synth.normal_bf16(c.seed, configs.TID_QW, (D,), mean=1.0, std=0.1)
+    g = synth.normal_bf16(c.seed, configs.TID_GATE, (Ts, I))
+    u = synth.normal_bf16(c.seed, configs.TID_UP, (Ts, I))
+    cache = oracle.build_rope_cache(Ts, D, configs.THETA)
+    nbytes = configs.chain_bytes(configs.Config("sample", 0, 1, Ts, H, I, c.heads_q, c.heads_kv, "range", Ts))
+
+    def one_pass(nt):
+        oracle.add_rms_norm(h1, d1, w1, EPS, band=False, nthreads=nt)
+        oracle.qk_norm_rope(q, qw, 1, Ts, c.heads_q, D, EPS, cache, band=False, nthreads=nt)
+        oracle.qk_norm_rope(k, qw, 1, Ts, c.heads_kv, D, EPS, cache, band=False, nthreads=nt)
+        oracle.add_rms_norm(h1, d1, w1, EPS, band=False, nthreads=nt)
+        oracle.silu_mul(g, u, band=False, nthreads=nt)
+
+    def rate(nt, budget):
+        one_pass(nt)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            one_pass(nt)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return nbytes * n / el / 1e9, n
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    multi, passes = rate(cores, seconds * 0.7)
+    single, _ = rate(1, seconds * 0.3)
+    return {
+        "value": round(multi, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": f"config-4 chain ops on the first {Ts} tokens ({nbytes} algorithmic bytes per pass), "
+                  f"{passes} passes on {cores} threads; oracle/q3k_oracle.c (C restatement of the reference's "
+                  f"CPU test arithmetic), host {platform.processor() or platform.machine()}",
+        "value_1thread": round(single, 3),
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); each op is token-local and would shard by tokens with no exchange.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    q3k = importlib.import_module(PKG)
+    hip = importlib.import_module(PKG + ".hip")
+    synth = importlib.import_module(PKG + ".synth")
+    configs = importlib.import_module(PKG + ".configs")
+    q3k.load()
+    if not hip.available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    c = configs.CONFIGS[args.config]
+    print(f"[bench] config {c.name}: generating inputs", file=sys.stderr, flush=True)
+
+    stream = hip.Stream()
+    base = make_chain_set(hip, synth, configs, c, q3k)
+    sets = [base] + [clone_set(hip, base) for _ in range(max(1, args.sets) - 1)]
+    print(f"[bench] timing chain: {args.warmup} warmup + {args.steps} steps over {len(sets)} sets",
+          file=sys.stderr, flush=True)
+    ms_step, per_op = time_ops(hip, stream, sets, lambda b: chain_ops(q3k, c, b, stream), args.steps, args.warmup)
+
+    T, H, I = c.tokens, c.hidden, c.inter
+    U = c.distinct_positions()
+    op_bytes = {
+        "add_rms_norm_attn": configs.bytes_add_rms_norm(T, H),
+        "qk_norm_rope": configs.bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, D, U),
+        "add_rms_norm_mlp": configs.bytes_add_rms_norm(T, H),
+        "silu_mul": configs.bytes_silu_mul(T, I),
+    }
+    chain_bytes = sum(op_bytes.values())
+    assert chain_bytes == configs.chain_bytes(c)
+    value = chain_bytes / (ms_step * 1e-3) / 1e9
+    ops_report = {}
+    for n, ms in per_op.items():
+        gbs = op_bytes[n] / (ms * 1e-3) / 1e9
+        ops_report[n] = {"ms": round(ms, 5), "bytes": op_bytes[n], "GB/s": round(gbs, 1),
+                         "pct_of_peak": round(100 * gbs / PEAK_GBS, 2)}
+    dominant = max(per_op, key=per_op.get)
+    dom_gbs = op_bytes[dominant] / (per_op[dominant] * 1e-3) / 1e9
+    kernel_key = {"silu_mul": "silu_mul", "qk_norm_rope": "qk_norm_rope"}.get(dominant, "add_rms_norm")
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(dom_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom_gbs / PEAK_GBS, 4), "traffic": read_traffic(kernel_key),
+                "algorithmic_bytes": op_bytes[dominant]}
+
+    extras = {}
+    if not args.no_extras:
+        print("[bench] timing unfused chain", file=sys.stderr, flush=True)
+        ms_unfused, per_unfused = time_ops(hip, stream, sets, lambda b: unfused_ops(q3k, c, b, stream),
+                                           max(5, args.steps // 2), 3)
+        extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5),
+                                   "per_op_ms": {k: round(v, 5) for k, v in per_unfused.items()},
+                                   "fused_speedup": round(ms_unfused / ms_step, 3)}
+        # final RMSNorm (model.cpp:146) at config 4, reading y1 of the rotating sets
+        fn_sets = sets
+        ms_rn, per_rn = time_ops(hip, stream, fn_sets, lambda b: [
+            ("rms_norm", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream))],
+            max(10, args.steps), 3)
+        rb = configs.bytes_rms_norm(T, H)
+        extras["rms_norm_final"] = {"ms": round(per_rn["rms_norm"], 5), "bytes": rb,
+                                    "GB/s": round(rb / (per_rn["rms_norm"] * 1e-3) / 1e9, 1)}
+        # copy ceiling: 1 GiB, 128-bit loads and stores
+        nb = 1 << 30
+        src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+        ms_cp, _ = time_ops(hip, stream, [0], lambda _: [("copy", lambda: q3k.bench_copy(src, dst, nb, stream))], 10, 2)
+        extras["copy_ceiling_GB/s"] = round(2 * nb / (ms_cp * 1e-3) / 1e9, 1)
+        src.free()
+        dst.free()
+        if "embedding" in c.ops:
+            print("[bench] timing embedding", file=sys.stderr, flush=True)
+            for s in sets[1:]:
+                for b in s.values():
+                    b.free()
+            table = hip.DeviceBuffer.from_array(
+                synth.normal_bf16(c.seed, configs.TID_TABLE, (configs.VOCAB, H)))
+            ids = hip.DeviceBuffer.from_array(synth.token_ids(c.seed, configs.TID_IDS, (T,), configs.VOCAB))
+            out = hip.DeviceBuffer(T * H * 2)
+            ms_e, _ = time_ops(hip, stream, [0], lambda _: [
+                ("embedding", lambda: q3k.embedding(ids, T, table, configs.VOCAB, H, out, stream))], 20, 3)
+            eb = configs.bytes_embedding(T, H)
+            extras["embedding"] = {"ms": round(ms_e, 5), "bytes": eb, "GB/s": round(eb / (ms_e * 1e-3) / 1e9, 1)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(configs, synth, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded normals, BASELINE config shapes)",
+        "config": {"workload": f"{c.name}: per-layer non-GEMM chain (add_rms_norm x2, qk_norm_rope, silu_mul)",
+                   "tokens": T, "hidden": H, "intermediate": I, "heads_q": c.heads_q, "heads_kv": c.heads_kv,
+                   "head_dim": D, "chain_bytes": chain_bytes, "input_sets": len(sets)},
+        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+        "tokens_per_s": round(T / (ms_step * 1e-3), 1),
+        "per_op": ops_report,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

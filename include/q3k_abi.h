@@ -1,0 +1,146 @@
+/*
+ * q3k_abi.h -- C ABI of the MI355X (gfx950) kernels for the Qwen3 decoder
+ * layer's non-GEMM ops.
+ *
+ * Every entry point takes plain device pointers and sizes, launches
+ * asynchronously on the given HIP stream (NULL = the legacy default stream,
+ * as the reference's ops use) and returns a q3k_status.  Nothing here
+ * allocates device memory, synchronises, switches the current device or
+ * throws.  The caller owns every buffer.  On a non-zero status the message is
+ * available from q3k_last_error_string() on the same host thread.
+ *
+ * Element types: bf16 buffers are uint16_t bit patterns (IEEE bfloat16),
+ * token ids and positions are int32_t, the RoPE table is float
+ * [positions, head_dim / 2, 2] with (cos, sin) pairs.
+ *
+ * Rounding contract (bf16 out, fp32 arithmetic, round-to-nearest-even at the
+ * same points as the reference kernels):
+ *   add          d = RNE(d + s)
+ *   rms_norm     y = RNE(RNE(x * inv) * w),  inv = 1 / sqrt(sum(x^2)/N + eps)
+ *   silu_mul     o = RNE(RNE(g / (1 + exp(-g))) * u)
+ *   rope         x1' = RNE(x1*c - x2*s), x2' = RNE(x2*c + x1*s), pairs (p, p + D/2)
+ *   add_rms_norm h = RNE(h + d); y = rms_norm(h) computed from the rounded h
+ *   qk_norm_rope per head: n = rms_norm(x) (two roundings), then rope(n)
+ */
+#ifndef Q3K_ABI_H
+#define Q3K_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define Q3K_API __attribute__((visibility("default")))
+#else
+#define Q3K_API
+#endif
+
+/* Same object as hipStream_t (a pointer to the runtime's opaque stream);
+ * declared here so that C callers need no HIP header. */
+struct ihipStream_t;
+typedef struct ihipStream_t *q3k_stream_t;
+
+typedef enum q3k_status {
+    Q3K_OK = 0,
+    Q3K_ERR_INVALID_ARGUMENT = 1, /* std::invalid_argument in the C++ ops layer */
+    Q3K_ERR_OUT_OF_RANGE = 2,     /* std::out_of_range */
+    Q3K_ERR_OVERFLOW = 3,         /* std::overflow_error */
+    Q3K_ERR_HIP = 4               /* std::runtime_error (HIP launch/runtime failure) */
+} q3k_status;
+
+/* Message for the last non-zero status returned on this host thread. */
+Q3K_API const char *q3k_last_error_string(void);
+
+/* Library version, "major.minor.patch". */
+Q3K_API const char *q3k_version(void);
+
+/*
+ * Embedding gather: out[t, :] = table[ids[t], :] for t in [0, T); a row of
+ * +0.0 for ids outside [0, V).  Bit-exact copy.
+ * Replaces qwen3::ops::embedding_lookup, src/ops/embedding.cu:85-149
+ * (kernel :23-55, out-of-range rule :38-45).
+ */
+Q3K_API int q3k_embedding_bf16(const int32_t *ids, int64_t T,
+                       const uint16_t *table, int64_t V, int64_t H,
+                       uint16_t *out, q3k_stream_t stream);
+
+/*
+ * RMSNorm over contiguous chunks of N elements: rows = numel / N.  N may be
+ * the head dimension of packed heads ([.., heads * N] with weight [N]).
+ * y must not overlap x.
+ * Replaces qwen3::ops::rms_norm, src/ops/rms_norm.cu:218-267 (kernel :69-127).
+ */
+Q3K_API int q3k_rms_norm_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y,
+                      int64_t rows, int64_t N, float eps, q3k_stream_t stream);
+
+/*
+ * Fused residual add + RMSNorm: h = RNE(h + d) written back in place, then
+ * y = rms_norm(h, w).  y must not overlap h or d.
+ * Replaces the pair add_inplace -> rms_norm at src/model/decoder_layer.cpp:78->88
+ * and :94 -> the next layer's :72 (or src/model/model.cpp:146 after the last
+ * layer); ops at src/ops/elementwise.cu:133-157 and src/ops/rms_norm.cu:218-267.
+ */
+Q3K_API int q3k_add_rms_norm_bf16(uint16_t *h, const uint16_t *d, const uint16_t *w,
+                          uint16_t *y, int64_t rows, int64_t N, float eps,
+                          q3k_stream_t stream);
+
+/*
+ * In-place residual add: d[i] = RNE(d[i] + s[i]), n elements.
+ * Replaces qwen3::ops::add_inplace, src/ops/elementwise.cu:133-157 (kernel :21-36).
+ */
+Q3K_API int q3k_add_inplace_bf16(uint16_t *d, const uint16_t *s, int64_t n,
+                         q3k_stream_t stream);
+
+/*
+ * SwiGLU activation: out[i] = RNE(RNE(silu(g[i])) * u[i]), n elements.
+ * out may alias g or u exactly (same pointer), not partially.
+ * Replaces qwen3::ops::silu_multiply, src/ops/elementwise.cu:159-190 (kernel :38-67).
+ */
+Q3K_API int q3k_silu_mul_bf16(const uint16_t *g, const uint16_t *u, uint16_t *out,
+                      int64_t n, q3k_stream_t stream);
+
+/*
+ * In-place half-split RoPE on x [B, S, heads * D].  Token (b, s) uses
+ * position positions[b * S + s] when positions != NULL, else start + s
+ * (the reference's scalar form).  The table has P positions; with the scalar
+ * form start + S must not exceed P (Q3K_ERR_OUT_OF_RANGE).  With a positions
+ * array, a head whose position lies outside [0, P) is overwritten with NaN
+ * (the kernel never reads outside the table).
+ * Replaces one launch_rope of qwen3::ops::apply_rope_inplace,
+ * src/ops/rope.cu:213-247 / :305-342 (kernel :21-86, range check :190-210).
+ */
+Q3K_API int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, int32_t D,
+                  const float *cache, int64_t P, int64_t start,
+                  const int32_t *positions, q3k_stream_t stream);
+
+/*
+ * Fused per-head Q/K RMSNorm + RoPE, in place, one pass over Q [B, S, Hq*D]
+ * and K [B, S, Hkv*D] with weights qw[D], kw[D].  Position rule and the
+ * out-of-range behaviour are those of q3k_rope_bf16.
+ * Replaces the sequence rms_norm(q) -> rms_norm(k) -> apply_rope_inplace at
+ * src/model/self_attention.cpp:147-152 (ops src/ops/rms_norm.cu:218-267,
+ * src/ops/rope.cu:305-342).
+ */
+Q3K_API int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k,
+                          const uint16_t *qw, const uint16_t *kw,
+                          int64_t B, int64_t S, int32_t Hq, int32_t Hkv,
+                          int32_t D, float eps,
+                          const float *cache, int64_t P, int64_t start,
+                          const int32_t *positions, q3k_stream_t stream);
+
+/*
+ * Host-side RoPE table: cache[p, i, 0] = (float)cos(p * theta^(-2i/D)),
+ * cache[p, i, 1] = (float)sin(...), evaluated in double, for p in [0, P),
+ * i in [0, D/2).  Writes P * D floats to host memory.  Same recipe and
+ * result as qwen3::ops::build_rope_cache, src/ops/rope.cu:250-303 (before
+ * its copy to the device).
+ */
+Q3K_API int q3k_build_rope_cache_f32(float *host_cache, int64_t P, int32_t D, float theta);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q3K_ABI_H */

@@ -1,0 +1,527 @@
+/*
+ * q3k_oracle.c -- CPU restatement of the reference runtime's non-GEMM layer
+ * arithmetic.  TEST INFRASTRUCTURE ONLY (see q3k_oracle.h): only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * Build: gcc -O2 -ffp-contract=off (see oracle/Makefile).  Contraction is
+ * off so that every fp32 product and sum below is rounded exactly where the
+ * source says; fmaf() marks the one place where the reference kernel is
+ * assumed to be contracted by nvcc (rms_norm.cu:89, "sum += v * v").
+ *
+ * Functions follow, and cite, the reference files under src/ops/.  CUDA's
+ * rsqrtf and expf cannot be restated bit for bit; the primary result uses
+ * the correctly rounded 1.0f/sqrtf(.) and (float)exp((double).), and the
+ * per-element band [lo, hi] covers the difference (q3k_oracle.h).
+ */
+#include "q3k_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- bf16 ------------------------------------------------------------- */
+
+uint16_t q3o_bf16_from_f32(float x)
+{
+    uint32_t b;
+    memcpy(&b, &x, sizeof b);
+    if ((b & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((b >> 16) | 0x0040u);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+float q3o_f32_from_bf16(uint16_t v)
+{
+    const uint32_t b = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &b, sizeof f);
+    return f;
+}
+
+#define BF q3o_bf16_from_f32
+#define FB q3o_f32_from_bf16
+
+static int is_nan_bf(uint16_t v) { return (v & 0x7fffu) > 0x7f80u; }
+
+static int32_t ord_bf(uint16_t v)
+{
+    return (v & 0x8000u) ? -(int32_t)(v & 0x7fffu) : (int32_t)v;
+}
+
+int32_t q3o_ulp_distance(uint16_t a, uint16_t b)
+{
+    const int na = is_nan_bf(a), nb = is_nan_bf(b);
+    if (na || nb)
+        return (na && nb) ? 0 : INT32_MAX;
+    const int32_t d = ord_bf(a) - ord_bf(b);
+    return d < 0 ? -d : d;
+}
+
+static uint16_t min_bf(uint16_t a, uint16_t b) { return ord_bf(a) <= ord_bf(b) ? a : b; }
+static uint16_t max_bf(uint16_t a, uint16_t b) { return ord_bf(a) >= ord_bf(b) ? a : b; }
+
+/* Relative half-widths of the fp32 noise bands.  2^-21 is 4..8 fp32 ulps:
+ * CUDA rsqrtf and expf are documented at <= 2 ulp, IEEE divide/sqrt add
+ * 0.5 ulp each, and any pairwise-ish fp32 sum of <= 8192 squares stays well
+ * inside the rest. */
+double q3o_band_rel_inv(void) { return ldexp(1.0, -21); }
+double q3o_band_rel_silu(void) { return ldexp(1.0, -21); }
+
+/* Spacing of fp32 values at |v| (as a double). */
+static double ulp_f32(double v)
+{
+    const float a = (float)fabs(v);
+    if (a == 0.0f)
+        return ldexp(1.0, -149);
+    if (isinf(a))
+        return INFINITY;
+    return (double)nextafterf(a, INFINITY) - (double)a;
+}
+
+/* bf16 of the fp32 rounding of a double (monotone in v). */
+static uint16_t bf_of_double(double v) { return BF((float)v); }
+
+/* ---- tiny parallel-for ----------------------------------------------- */
+
+typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
+
+struct par_job
+{
+    range_fn fn;
+    void *ctx;
+    int64_t begin, end;
+};
+
+static void *par_entry(void *arg)
+{
+    struct par_job *j = (struct par_job *)arg;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+
+static void parallel_for(int64_t n, int nthreads, range_fn fn, void *ctx)
+{
+    if (nthreads <= 1 || n < 2)
+    {
+        fn(ctx, 0, n);
+        return;
+    }
+    if (nthreads > 256)
+        nthreads = 256;
+    if ((int64_t)nthreads > n)
+        nthreads = (int)n;
+    pthread_t tid[256];
+    struct par_job jobs[256];
+    int started[256];
+    for (int t = 0; t < nthreads; ++t)
+    {
+        jobs[t].fn = fn;
+        jobs[t].ctx = ctx;
+        jobs[t].begin = n * t / nthreads;
+        jobs[t].end = n * (t + 1) / nthreads;
+        started[t] = (t > 0) && pthread_create(&tid[t], NULL, par_entry, &jobs[t]) == 0;
+    }
+    fn(ctx, jobs[0].begin, jobs[0].end);
+    for (int t = 1; t < nthreads; ++t)
+    {
+        if (started[t])
+            pthread_join(tid[t], NULL);
+        else
+            fn(ctx, jobs[t].begin, jobs[t].end);
+    }
+}
+
+/* ---- embedding: src/ops/embedding.cu:29-54 ----------------------------- */
+
+struct emb_ctx
+{
+    const int32_t *ids;
+    const uint16_t *table;
+    int64_t V, H;
+    uint16_t *out;
+};
+
+static void emb_range(void *p, int64_t b, int64_t e)
+{
+    const struct emb_ctx *c = (const struct emb_ctx *)p;
+    for (int64_t t = b; t < e; ++t)
+    {
+        const int32_t id = c->ids[t];
+        uint16_t *dst = c->out + t * c->H;
+        if (id < 0 || (int64_t)id >= c->V)
+            memset(dst, 0, (size_t)c->H * sizeof(uint16_t)); /* __float2bfloat16(0.0F) */
+        else
+            memcpy(dst, c->table + (int64_t)id * c->H, (size_t)c->H * sizeof(uint16_t));
+    }
+}
+
+void q3o_embedding(const int32_t *ids, int64_t T, const uint16_t *table, int64_t V, int64_t H,
+                   uint16_t *out, int nthreads)
+{
+    struct emb_ctx c = {ids, table, V, H, out};
+    parallel_for(T, nthreads, emb_range, &c);
+}
+
+/* ---- add: src/ops/elementwise.cu:28-35 --------------------------------- */
+
+struct add_ctx
+{
+    uint16_t *d;
+    const uint16_t *s;
+};
+
+static void add_range(void *p, int64_t b, int64_t e)
+{
+    const struct add_ctx *c = (const struct add_ctx *)p;
+    for (int64_t i = b; i < e; ++i)
+        c->d[i] = BF(FB(c->d[i]) + FB(c->s[i]));
+}
+
+void q3o_add_inplace(uint16_t *d, const uint16_t *s, int64_t n, int nthreads)
+{
+    struct add_ctx c = {d, s};
+    parallel_for(n, nthreads, add_range, &c);
+}
+
+/* ---- rms_norm: src/ops/rms_norm.cu:22-67, 82-121 ----------------------- */
+
+/* Lane 0 of __shfl_down_sync tree over 32 lanes (rms_norm.cu:22-30). */
+static float warp_tree(const float *in)
+{
+    float v[32];
+    memcpy(v, in, sizeof v);
+    for (int off = 16; off > 0; off >>= 1)
+        for (int i = 0; i < off; ++i)
+            v[i] = v[i] + v[i + off];
+    return v[0];
+}
+
+/* Sum of squares in the reference kernel's order: 256 threads, thread j
+ * accumulates columns j, j+256, ... (rms_norm.cu:85-90, contracted), then
+ * the per-warp trees and the tree over the 8 warp partials (:32-67). */
+static float ref_sum_squares(const uint16_t *x, int64_t n)
+{
+    float part[256];
+    for (int j = 0; j < 256; ++j)
+    {
+        float p = 0.0f;
+        for (int64_t c = j; c < n; c += 256)
+        {
+            const float v = FB(x[c]);
+            p = fmaf(v, v, p);
+        }
+        part[j] = p;
+    }
+    float block[32];
+    memset(block, 0, sizeof block);
+    for (int w = 0; w < 8; ++w)
+        block[w] = warp_tree(part + 32 * w);
+    return warp_tree(block);
+}
+
+/* Normalise one row.  x_row holds the (already rounded) bf16 inputs. */
+static void rms_row(const uint16_t *x, const uint16_t *w, int64_t n, float eps, uint16_t *y, uint16_t *lo,
+                    uint16_t *hi)
+{
+    const float sum = ref_sum_squares(x, n);
+    const float mean = sum / (float)n;
+    const float inv = 1.0f / sqrtf(mean + eps); /* stands in for rsqrtf (rms_norm.cu:98) */
+
+    for (int64_t c = 0; c < n; ++c)
+    {
+        const uint16_t nrm = BF(FB(x[c]) * inv);
+        y[c] = BF(FB(nrm) * FB(w[c]));
+    }
+    if (lo == NULL || hi == NULL)
+        return;
+
+    double exact = 0.0;
+    for (int64_t c = 0; c < n; ++c)
+    {
+        const double v = FB(x[c]);
+        exact += v * v;
+    }
+    const double inv_exact = 1.0 / sqrt(exact / (double)n + (double)eps);
+    const double rel = q3o_band_rel_inv();
+    const double a = fmin((double)inv, inv_exact) * (1.0 - rel);
+    const double b = fmax((double)inv, inv_exact) * (1.0 + rel);
+    for (int64_t c = 0; c < n; ++c)
+    {
+        const double xv = FB(x[c]);
+        const uint16_t na = bf_of_double(xv * a), nb = bf_of_double(xv * b);
+        const uint16_t nprim = BF(FB(x[c]) * inv);
+        const uint16_t nlo = min_bf(min_bf(na, nb), nprim), nhi = max_bf(max_bf(na, nb), nprim);
+        const float wv = FB(w[c]);
+        const uint16_t ya = BF(FB(nlo) * wv), yb = BF(FB(nhi) * wv);
+        lo[c] = min_bf(min_bf(ya, yb), y[c]);
+        hi[c] = max_bf(max_bf(ya, yb), y[c]);
+    }
+}
+
+struct rms_ctx
+{
+    uint16_t *h;
+    const uint16_t *x, *d, *w;
+    int64_t n;
+    float eps;
+    uint16_t *y, *lo, *hi;
+};
+
+static void rms_range(void *p, int64_t b, int64_t e)
+{
+    const struct rms_ctx *c = (const struct rms_ctx *)p;
+    for (int64_t r = b; r < e; ++r)
+    {
+        const int64_t off = r * c->n;
+        const uint16_t *src = c->x + off;
+        if (c->d != NULL)
+        {
+            /* residual add first (elementwise.cu:34), the norm reads the rounded h */
+            for (int64_t i = 0; i < c->n; ++i)
+                c->h[off + i] = BF(FB(c->h[off + i]) + FB(c->d[off + i]));
+            src = c->h + off;
+        }
+        rms_row(src, c->w, c->n, c->eps, c->y + off, c->lo ? c->lo + off : NULL, c->hi ? c->hi + off : NULL);
+    }
+}
+
+void q3o_rms_norm(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t N, float eps, uint16_t *y,
+                  uint16_t *lo, uint16_t *hi, int nthreads)
+{
+    struct rms_ctx c = {NULL, x, NULL, w, N, eps, y, lo, hi};
+    parallel_for(rows, nthreads, rms_range, &c);
+}
+
+void q3o_add_rms_norm(uint16_t *h, const uint16_t *d, const uint16_t *w, int64_t rows, int64_t N, float eps,
+                      uint16_t *y, uint16_t *lo, uint16_t *hi, int nthreads)
+{
+    struct rms_ctx c = {h, h, d, w, N, eps, y, lo, hi};
+    parallel_for(rows, nthreads, rms_range, &c);
+}
+
+/* ---- silu(gate) * up: src/ops/elementwise.cu:45-66 ----------------------- */
+
+struct silu_ctx
+{
+    const uint16_t *g, *u;
+    uint16_t *out, *lo, *hi;
+};
+
+static void silu_range(void *p, int64_t b, int64_t e)
+{
+    const struct silu_ctx *c = (const struct silu_ctx *)p;
+    const double rel = q3o_band_rel_silu();
+    for (int64_t i = b; i < e; ++i)
+    {
+        const float g = FB(c->g[i]);
+        const float u = FB(c->u[i]);
+        const float ex = (float)exp(-(double)g); /* stands in for expf (elementwise.cu:51) */
+        const float den = 1.0f + ex;
+        const float s = g / den;
+        const uint16_t n = BF(s);
+        c->out[i] = BF(FB(n) * u);
+        if (c->lo == NULL || c->hi == NULL)
+            continue;
+        double sx;
+        const double E = exp(-(double)g);
+        if (isinf((float)E))
+            sx = (double)g / INFINITY; /* fp32 exp overflows: silu is a signed zero */
+        else
+            sx = (double)g / (1.0 + E);
+        const uint16_t na = bf_of_double(sx * (1.0 - rel)), nb = bf_of_double(sx * (1.0 + rel));
+        const uint16_t nlo = min_bf(min_bf(na, nb), n), nhi = max_bf(max_bf(na, nb), n);
+        const uint16_t oa = BF(FB(nlo) * u), ob = BF(FB(nhi) * u);
+        c->lo[i] = min_bf(min_bf(oa, ob), c->out[i]);
+        c->hi[i] = max_bf(max_bf(oa, ob), c->out[i]);
+    }
+}
+
+void q3o_silu_mul(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *out, uint16_t *lo, uint16_t *hi,
+                  int nthreads)
+{
+    struct silu_ctx c = {g, u, out, lo, hi};
+    parallel_for(n, nthreads, silu_range, &c);
+}
+
+/* ---- rope: src/ops/rope.cu:38-85, 267-296 -------------------------------- */
+
+int q3o_build_rope_cache(int64_t P, int32_t D, float theta, float *cache)
+{
+    if (P <= 0 || D <= 0 || (D % 2) != 0 || !(theta > 0.0f) || isinf(theta) || cache == NULL)
+        return -1;
+    const int64_t half = D / 2;
+    double *inv = (double *)malloc((size_t)half * sizeof(double));
+    if (inv == NULL)
+        return -1;
+    for (int64_t i = 0; i < half; ++i)
+        inv[i] = pow((double)theta, -((2.0 * (double)i) / (double)D));
+    for (int64_t p = 0; p < P; ++p)
+        for (int64_t i = 0; i < half; ++i)
+        {
+            const double angle = (double)p * inv[i];
+            cache[(p * half + i) * 2] = (float)cos(angle);
+            cache[(p * half + i) * 2 + 1] = (float)sin(angle);
+        }
+    free(inv);
+    return 0;
+}
+
+/* Interval [lo, hi] of bf16 values for v1 * c + v2 * s2 with v1 in
+ * [a_lo, a_hi], v2 in [b_lo, b_hi] (fp32 values), widened by the rounding
+ * of the two products and the sum in any contraction order (1.5 ulp of the
+ * larger product). */
+static void rot_band(float a_lo, float a_hi, float c, float b_lo, float b_hi, float s2, uint16_t prim,
+                     uint16_t *lo, uint16_t *hi)
+{
+    const double p1 = (double)a_lo * c, p2 = (double)a_hi * c;
+    const double q1 = (double)b_lo * s2, q2 = (double)b_hi * s2;
+    const double mn = fmin(p1, p2) + fmin(q1, q2);
+    const double mx = fmax(p1, p2) + fmax(q1, q2);
+    const double big = fmax(fmax(fabs(p1), fabs(p2)), fmax(fabs(q1), fabs(q2)));
+    const double err = 1.5 * ulp_f32(big);
+    *lo = min_bf(bf_of_double(mn - err), prim);
+    *hi = max_bf(bf_of_double(mx + err), prim);
+}
+
+struct rope_ctx
+{
+    uint16_t *x;
+    const uint16_t *w; /* non-NULL: fused norm first */
+    int64_t S;
+    int32_t heads, D;
+    float eps;
+    const float *cache;
+    int64_t P, start;
+    const int32_t *positions;
+    uint16_t *lo, *hi;
+};
+
+static void rope_range(void *p, int64_t b, int64_t e)
+{
+    const struct rope_ctx *c = (const struct rope_ctx *)p;
+    const int64_t D = c->D, half = D / 2;
+    uint16_t *nrm = (uint16_t *)malloc((size_t)D * 3 * sizeof(uint16_t));
+    if (nrm == NULL)
+        abort();
+    uint16_t *nlo = nrm + D, *nhi = nrm + 2 * D;
+    for (int64_t t = b; t < e; ++t)
+    {
+        const int64_t pos = c->positions ? (int64_t)c->positions[t] : c->start + t % c->S;
+        for (int32_t hd = 0; hd < c->heads; ++hd)
+        {
+            uint16_t *head = c->x + (t * c->heads + hd) * D;
+            uint16_t *hlo = c->lo ? c->lo + (t * c->heads + hd) * D : NULL;
+            uint16_t *hhi = c->hi ? c->hi + (t * c->heads + hd) * D : NULL;
+            if (pos < 0 || pos >= c->P)
+            {
+                for (int64_t i = 0; i < D; ++i)
+                {
+                    head[i] = 0x7fc0;
+                    if (hlo)
+                        hlo[i] = hhi[i] = 0x7fc0;
+                }
+                continue;
+            }
+            if (c->w != NULL)
+            {
+                /* self_attention.cpp:147-149: rms_norm over the head, two roundings */
+                rms_row(head, c->w, D, c->eps, nrm, hlo ? nlo : NULL, hlo ? nhi : NULL);
+                memcpy(head, nrm, (size_t)D * sizeof(uint16_t));
+            }
+            else if (hlo)
+            {
+                memcpy(nlo, head, (size_t)D * sizeof(uint16_t));
+                memcpy(nhi, head, (size_t)D * sizeof(uint16_t));
+            }
+            for (int64_t i = 0; i < half; ++i)
+            {
+                const float cs = c->cache[(pos * half + i) * 2];
+                const float sn = c->cache[(pos * half + i) * 2 + 1];
+                const float x1 = FB(head[i]), x2 = FB(head[i + half]);
+                const float a = x1 * cs, bb = x2 * sn, ee = x2 * cs, ff = x1 * sn;
+                const uint16_t o1 = BF(a - bb), o2 = BF(ee + ff);
+                if (hlo)
+                {
+                    rot_band(FB(nlo[i]), FB(nhi[i]), cs, FB(nlo[i + half]), FB(nhi[i + half]), -sn, o1, &hlo[i],
+                             &hhi[i]);
+                    rot_band(FB(nlo[i + half]), FB(nhi[i + half]), cs, FB(nlo[i]), FB(nhi[i]), sn, o2,
+                             &hlo[i + half], &hhi[i + half]);
+                }
+                head[i] = o1;
+                head[i + half] = o2;
+            }
+        }
+    }
+    free(nrm);
+}
+
+static int rope_common(uint16_t *x, const uint16_t *w, int64_t B, int64_t S, int32_t heads, int32_t D, float eps,
+                       const float *cache, int64_t P, int64_t start, const int32_t *positions, uint16_t *lo,
+                       uint16_t *hi, int nthreads)
+{
+    if (B < 0 || S < 0 || heads <= 0 || D <= 0 || D % 2 != 0 || P <= 0)
+        return -1;
+    if (positions == NULL && (start < 0 || start > P || S > P - start))
+        return -1;
+    if ((lo == NULL) != (hi == NULL))
+        return -1;
+    struct rope_ctx c = {x, w, S, heads, D, eps, cache, P, start, positions, lo, hi};
+    parallel_for(B * S, nthreads, rope_range, &c);
+    return 0;
+}
+
+int q3o_rope(uint16_t *x, int64_t B, int64_t S, int32_t heads, int32_t D, const float *cache, int64_t P,
+             int64_t start, const int32_t *positions, uint16_t *lo, uint16_t *hi, int nthreads)
+{
+    return rope_common(x, NULL, B, S, heads, D, 0.0f, cache, P, start, positions, lo, hi, nthreads);
+}
+
+int q3o_qk_norm_rope(uint16_t *x, const uint16_t *w, int64_t B, int64_t S, int32_t heads, int32_t D, float eps,
+                     const float *cache, int64_t P, int64_t start, const int32_t *positions, uint16_t *lo,
+                     uint16_t *hi, int nthreads)
+{
+    if (w == NULL)
+        return -1;
+    return rope_common(x, w, B, S, heads, D, eps, cache, P, start, positions, lo, hi, nthreads);
+}
+
+/* ---- comparison ----------------------------------------------------------- */
+
+void q3o_compare_band(const uint16_t *got, const uint16_t *primary, const uint16_t *lo, const uint16_t *hi,
+                      int64_t n, int64_t *stats)
+{
+    for (int i = 0; i < 8; ++i)
+        stats[i] = 0;
+    stats[0] = n;
+    stats[2] = -1;
+    for (int64_t i = 0; i < n; ++i)
+    {
+        const uint16_t l = lo ? lo[i] : primary[i];
+        const uint16_t h = hi ? hi[i] : primary[i];
+        const int32_t dist = q3o_ulp_distance(got[i], primary[i]);
+        if (dist == 0)
+            stats[4]++;
+        else if (dist == 1)
+            stats[5]++;
+        else if (dist == 2)
+            stats[6]++;
+        else
+            stats[7]++;
+        if (ord_bf(l) != ord_bf(h))
+            stats[3]++;
+        int ok;
+        if (is_nan_bf(got[i]) || is_nan_bf(primary[i]))
+            ok = is_nan_bf(got[i]) && is_nan_bf(primary[i]);
+        else
+            ok = ord_bf(got[i]) >= ord_bf(l) - 1 && ord_bf(got[i]) <= ord_bf(h) + 1;
+        if (!ok)
+        {
+            if (stats[2] < 0)
+                stats[2] = i;
+            stats[1]++;
+        }
+    }
+}

@@ -1,0 +1,176 @@
+"""Python view of the gfx950 kernel library ``lib/libq3k.so``.
+
+The product is the C ABI in ``include/q3k_abi.h`` (plain device pointers,
+sizes and a HIP stream) and the C++ ``qwen3::ops`` layer above it.  This
+module binds the same entry points through ctypes for the test suite, the
+benchmark and ``__graft_entry__``; each wrapper keeps the argument order of
+the C function and turns a non-zero status into the exception the C++ layer
+throws (``std::invalid_argument`` -> ValueError, ``std::out_of_range`` ->
+IndexError, ``std::overflow_error`` -> OverflowError, HIP failures ->
+RuntimeError).
+
+There is no fallback: if the library is not built, :func:`load` raises.
+Device memory comes from :mod:`.hip` (the HIP runtime the library links).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libq3k.so")
+RUNTIME_LIB_PATH = os.path.join(LIB_DIR, "libqwen3_runtime.so")
+ABI_HEADERS = [os.path.join(REPO_DIR, "include", "q3k_abi.h"), os.path.join(REPO_DIR, "include", "q3k_bench.h")]
+
+Q3K_OK = 0
+Q3K_ERR_INVALID_ARGUMENT = 1
+Q3K_ERR_OUT_OF_RANGE = 2
+Q3K_ERR_OVERFLOW = 3
+Q3K_ERR_HIP = 4
+
+
+class Q3kError(RuntimeError):
+    """A non-zero q3k_status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class Q3kInvalidArgument(Q3kError, ValueError):
+    pass
+
+
+class Q3kOutOfRange(Q3kError, IndexError):
+    pass
+
+
+class Q3kOverflow(Q3kError, OverflowError):
+    pass
+
+
+class Q3kHipError(Q3kError):
+    pass
+
+
+_ERRORS = {
+    Q3K_ERR_INVALID_ARGUMENT: Q3kInvalidArgument,
+    Q3K_ERR_OUT_OF_RANGE: Q3kOutOfRange,
+    Q3K_ERR_OVERFLOW: Q3kOverflow,
+    Q3K_ERR_HIP: Q3kHipError,
+}
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+# name -> argtypes, in the order of include/q3k_abi.h
+SIGNATURES = {
+    "q3k_embedding_bf16": [_p, _i64, _p, _i64, _i64, _p, _p],
+    "q3k_rms_norm_bf16": [_p, _p, _p, _i64, _i64, _f32, _p],
+    "q3k_add_rms_norm_bf16": [_p, _p, _p, _p, _i64, _i64, _f32, _p],
+    "q3k_add_inplace_bf16": [_p, _p, _i64, _p],
+    "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
+    "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
+    "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
+    "q3k_build_rope_cache_f32": [_p, _i64, _i32, _f32],
+    "q3k_bench_copy_u128": [_p, _p, _i64, _p],
+}
+
+_lib = None
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in the public C headers."""
+    names = []
+    for path in ABI_HEADERS:
+        with open(path) as f:
+            text = f.read()
+        names += re.findall(r"Q3K_API\s+[\w\s\*]*?\b(q3k_\w+)\s*\(", text)
+    return names
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load libq3k.so (RTLD_GLOBAL, so that :mod:`.hip` binds the same HIP runtime)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    lib_path = path or LIB_PATH
+    if not os.path.exists(lib_path):
+        raise RuntimeError(
+            f"{lib_path} is not built; run __graft_entry__.build() (the HIP kernels have no fallback)")
+    lib = ctypes.CDLL(lib_path, mode=ctypes.RTLD_GLOBAL)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.q3k_last_error_string.restype = ctypes.c_char_p
+    lib.q3k_last_error_string.argtypes = []
+    lib.q3k_version.restype = ctypes.c_char_p
+    lib.q3k_version.argtypes = []
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != Q3K_OK:
+        msg = load().q3k_last_error_string().decode()
+        raise _ERRORS.get(status, Q3kError)(status, msg)
+
+
+def _ptr(x):
+    """Device address of a buffer object (anything with ``.ptr``) or an int."""
+    if x is None:
+        return None
+    return getattr(x, "ptr", x)
+
+
+def version() -> str:
+    return load().q3k_version().decode()
+
+
+def embedding(ids, T, table, V, H, out, stream=None):
+    _check(load().q3k_embedding_bf16(_ptr(ids), T, _ptr(table), V, H, _ptr(out), _ptr(stream)))
+
+
+def rms_norm(x, w, y, rows, N, eps, stream=None):
+    _check(load().q3k_rms_norm_bf16(_ptr(x), _ptr(w), _ptr(y), rows, N, eps, _ptr(stream)))
+
+
+def add_rms_norm(h, d, w, y, rows, N, eps, stream=None):
+    _check(load().q3k_add_rms_norm_bf16(_ptr(h), _ptr(d), _ptr(w), _ptr(y), rows, N, eps, _ptr(stream)))
+
+
+def add_inplace(d, s, n, stream=None):
+    _check(load().q3k_add_inplace_bf16(_ptr(d), _ptr(s), n, _ptr(stream)))
+
+
+def silu_mul(g, u, out, n, stream=None):
+    _check(load().q3k_silu_mul_bf16(_ptr(g), _ptr(u), _ptr(out), n, _ptr(stream)))
+
+
+def rope(x, B, S, heads, D, cache, P, start, positions=None, stream=None):
+    _check(load().q3k_rope_bf16(_ptr(x), B, S, heads, D, _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
+
+
+def qk_norm_rope(q, k, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, positions=None, stream=None):
+    _check(load().q3k_qk_norm_rope_bf16(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw), B, S, Hq, Hkv, D, eps,
+                                        _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
+
+
+def build_rope_cache(P: int, D: int, theta: float):
+    """Host RoPE table [P, D/2, 2] as a float32 numpy array."""
+    import numpy as np
+
+    out = np.empty((P, D // 2, 2), dtype=np.float32)
+    _check(load().q3k_build_rope_cache_f32(out.ctypes.data, P, D, theta))
+    return out
+
+
+def bench_copy(src, dst, nbytes, stream=None):
+    _check(load().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))

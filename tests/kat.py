@@ -1,0 +1,54 @@
+"""Known-answer inputs of the reference's GPU op tests, restated as data
+generators (closed-form integer patterns, exactly representable in bf16).
+
+Sources (reference tests/unit/):
+  rms_norm_cuda_test.cpp:111-141    x[i] = ((i % 31) - 15) * 0.125, w[j] = 0.5 + (j % 17) * 0.03125
+  rope_cuda_test.cpp:38-58, 210-241 v[i] = ((i + off) % 17 - 8) * 0.25, off 0 (Q) / 5 (K)
+  elementwise_cuda_test.cpp:138-181 residual ((i%41)-20)/16, delta ((i%17)-8)/32,
+                                    gate ((i%37)-18)/4, up ((i%23)-11)/8
+  embedding_cuda_test.cpp:102-143   W[t, h] = 10 t + h, ids [[2,0,4],[1,2,3]]
+"""
+import numpy as np
+
+
+def bf(values):
+    """Exact float -> bf16 bits for values representable in bf16."""
+    v = np.asarray(values, dtype=np.float32)
+    b = v.view(np.uint32)
+    assert np.all((b & 0xFFFF) == 0), "KAT value not exact in bf16"
+    return (b >> 16).astype(np.uint16)
+
+
+def rms_input(shape):
+    n = int(np.prod(shape))
+    i = np.arange(n)
+    return bf(((i % 31) - 15) * 0.125).reshape(shape)
+
+
+def rms_weight(hidden):
+    j = np.arange(hidden)
+    return bf(0.5 + (j % 17) * 0.03125)
+
+
+def rope_values(n, offset):
+    i = np.arange(n)
+    return bf((((i + offset) % 17) - 8) * 0.25)
+
+
+def elementwise_inputs(shape=(2, 3, 257)):
+    n = int(np.prod(shape))
+    i = np.arange(n)
+    return (bf(((i % 41) - 20) * 0.0625).reshape(shape), bf(((i % 17) - 8) * 0.03125).reshape(shape),
+            bf(((i % 37) - 18) * 0.25).reshape(shape), bf(((i % 23) - 11) * 0.125).reshape(shape))
+
+
+def embedding_inputs():
+    V, H = 5, 4
+    t, h = np.meshgrid(np.arange(V), np.arange(H), indexing="ij")
+    table = bf((t * 10 + h).astype(np.float32))
+    ids = np.array([[2, 0, 4], [1, 2, 3]], dtype=np.int32)
+    return table, ids
+
+
+# RoPE KAT constants (rope_cuda_test.cpp:210-220)
+ROPE_B, ROPE_S, ROPE_HQ, ROPE_HKV, ROPE_D, ROPE_P, ROPE_START, ROPE_THETA = 1, 3, 2, 1, 8, 16, 5, 1.0e6

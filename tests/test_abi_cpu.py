@@ -1,0 +1,108 @@
+"""The C ABI library on the CPU: it loads, exports what the headers declare,
+and rejects bad arguments with the documented status before touching the GPU.
+No kernel is launched here."""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+
+def test_library_exports_every_declared_symbol(q3k):
+    lib = q3k.load()
+    declared = q3k.declared_symbols()
+    assert len(declared) >= 11
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert set(declared) == set(q3k.SIGNATURES) | {"q3k_last_error_string", "q3k_version"}
+
+
+def test_exports_are_only_the_abi(q3k):
+    out = subprocess.run(["nm", "-D", "--defined-only", q3k.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    assert exported == set(q3k.declared_symbols())
+
+
+def test_version(q3k):
+    assert q3k.version().count(".") == 2
+
+
+def _expect(fn, exc, status, *args):
+    with pytest.raises(exc) as info:
+        fn(*args)
+    assert info.value.status == status
+    return str(info.value)
+
+
+def test_argument_errors_without_gpu(q3k):
+    IA, OR, OV = q3k.Q3K_ERR_INVALID_ARGUMENT, q3k.Q3K_ERR_OUT_OF_RANGE, q3k.Q3K_ERR_OVERFLOW
+    fake = 256  # never dereferenced: every call below fails validation first
+    # rms_norm: eps must be finite and positive (rms_norm.cu:209-214), N positive
+    msg = _expect(q3k.rms_norm, ValueError, IA, fake, fake, fake, 4, 128, 0.0)
+    assert "epsilon" in msg
+    _expect(q3k.rms_norm, ValueError, IA, fake, fake, fake, 4, 128, float("nan"))
+    _expect(q3k.rms_norm, ValueError, IA, fake, fake, fake, 4, 128, float("inf"))
+    _expect(q3k.rms_norm, ValueError, IA, fake, fake, fake, 4, 0, 1e-6)
+    _expect(q3k.rms_norm, ValueError, IA, None, fake, fake, 4, 128, 1e-6)
+    _expect(q3k.rms_norm, OverflowError, OV, fake, fake, fake, 2**62, 2**10, 1e-6)
+    _expect(q3k.add_rms_norm, ValueError, IA, fake, None, fake, fake, 4, 128, 1e-6)
+    # elementwise
+    _expect(q3k.silu_mul, ValueError, IA, fake, fake, None, 8)
+    _expect(q3k.silu_mul, ValueError, IA, fake, fake, fake, -1)
+    _expect(q3k.add_inplace, ValueError, IA, None, fake, 8)
+    # embedding
+    _expect(q3k.embedding, ValueError, IA, fake, 4, fake, 0, 8, fake)
+    _expect(q3k.embedding, ValueError, IA, None, 4, fake, 10, 8, fake)
+    # rope: negative start (rope.cu:190-194), range past the table (rope.cu:204-210)
+    _expect(q3k.rope, ValueError, IA, fake, 1, 3, 2, 8, fake, 16, -1)
+    msg = _expect(q3k.rope, IndexError, OR, fake, 1, 3, 2, 8, fake, 16, 15)
+    assert "exceeds" in msg
+    _expect(q3k.rope, ValueError, IA, fake, 1, 3, 0, 8, fake, 16, 0)
+    _expect(q3k.rope, ValueError, IA, fake, 1, 3, 2, 7, fake, 16, 0)
+    _expect(q3k.qk_norm_rope, IndexError, OR, fake, fake, fake, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 14)
+    _expect(q3k.qk_norm_rope, ValueError, IA, fake, fake, fake, fake, 1, 3, 2, 1, 8, -1.0, fake, 16, 0)
+    _expect(q3k.qk_norm_rope, ValueError, IA, fake, fake, None, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 0)
+    # copy helper
+    _expect(q3k.bench_copy, ValueError, IA, fake, fake, 15)
+
+
+def test_empty_inputs_are_no_ops(q3k):
+    # zero work returns OK without a launch (no GPU needed)
+    q3k.rms_norm(None, None, None, 0, 128, 1e-6)
+    q3k.add_rms_norm(None, None, None, None, 0, 128, 1e-6)
+    q3k.silu_mul(None, None, None, 0)
+    q3k.add_inplace(None, None, 0)
+    q3k.embedding(None, 0, None, 10, 8, None)
+    q3k.rope(None, 0, 5, 2, 8, None, 16, 0)
+    q3k.qk_norm_rope(None, None, None, None, 3, 0, 2, 1, 8, 1e-6, None, 16, 0)
+
+
+def test_rope_cache_builder_matches_oracle(q3k, oracle):
+    for P, D, theta in ((16, 8, 1.0e6), (2048, 128, 1.0e6), (33, 64, 10000.0)):
+        ours = q3k.build_rope_cache(P, D, theta)
+        ref = oracle.build_rope_cache(P, D, theta)
+        assert ours.shape == (P, D // 2, 2)
+        assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+    with pytest.raises(ValueError):
+        q3k.build_rope_cache(0, 128, 1e6)
+    with pytest.raises(ValueError):
+        q3k.build_rope_cache(4, 7, 1e6)
+    with pytest.raises(ValueError):
+        q3k.build_rope_cache(4, 8, float("inf"))
+
+
+def test_error_string_is_thread_local(q3k):
+    import threading
+
+    lib = q3k.load()
+    lib.q3k_rms_norm_bf16(None, None, None, 1, 0, ctypes.c_float(1e-6), None)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.q3k_last_error_string().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == "no error"
+    assert "normalized size" in lib.q3k_last_error_string().decode()

@@ -1,0 +1,314 @@
+"""Parity of the gfx950 kernels (through the C ABI) with the CPU oracle.
+
+Bar: embedding and add bit-exact; every other bf16 output inside the
+oracle's band widened by 1 bf16 ulp (q3k_oracle.h), i.e. within 1 ulp of a
+result the reference's fp32 arithmetic can produce.  Every device buffer
+carries guard bands that must be intact afterwards (no out-of-bounds
+writes).  Shapes cover the reference tests' known answers, odd sizes that
+take the generic kernels, unaligned pointers, empty inputs, out-of-range ids
+and positions, and small slices of every benchmark config; the full-size
+configs are in test_gpu_configs.py.
+"""
+import numpy as np
+import pytest
+
+import kat
+from gpu_util import Guarded, announce, check_band, check_exact
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+# ---------------------------------------------------------------- runners ---
+
+def run_rms(q3k, hip, x, w, eps=EPS, offset=0):
+    N = w.size
+    rows = x.size // N
+    X, W, Y = Guarded(hip, x, offset=offset), Guarded(hip, w, offset=offset), Guarded(hip, nbytes=x.nbytes, offset=offset)
+    q3k.rms_norm(X, W, Y, rows, N, eps)
+    hip.synchronize()
+    y = Y.get(np.uint16, x.shape)
+    assert X.guards_intact() and W.guards_intact() and Y.guards_intact()
+    assert np.array_equal(X.get(np.uint16, x.shape), x), "rms_norm modified its input"
+    return y
+
+
+def run_add_rms(q3k, hip, h, d, w, eps=EPS, offset=0):
+    N = w.size
+    rows = h.size // N
+    H, D, W = Guarded(hip, h, offset=offset), Guarded(hip, d, offset=offset), Guarded(hip, w, offset=offset)
+    Y = Guarded(hip, nbytes=h.nbytes, offset=offset)
+    q3k.add_rms_norm(H, D, W, Y, rows, N, eps)
+    hip.synchronize()
+    out = H.get(np.uint16, h.shape), Y.get(np.uint16, h.shape)
+    assert all(b.guards_intact() for b in (H, D, W, Y))
+    return out
+
+
+def run_binary(q3k, hip, op, a, b, offset=0):
+    A, B = Guarded(hip, a, offset=offset), Guarded(hip, b, offset=offset)
+    if op == "silu":
+        O = Guarded(hip, nbytes=a.nbytes, offset=offset)
+        q3k.silu_mul(A, B, O, a.size)
+    else:
+        O = A
+        q3k.add_inplace(A, B, a.size)
+    hip.synchronize()
+    out = O.get(np.uint16, a.shape)
+    assert A.guards_intact() and B.guards_intact() and O.guards_intact()
+    return out
+
+
+def run_embedding(q3k, hip, ids, table, offset=0):
+    V, H = table.shape
+    I, Tb = Guarded(hip, ids), Guarded(hip, table, offset=offset)
+    O = Guarded(hip, nbytes=ids.size * H * 2, offset=offset)
+    q3k.embedding(I, ids.size, Tb, V, H, O)
+    hip.synchronize()
+    out = O.get(np.uint16, ids.shape + (H,))
+    assert I.guards_intact() and Tb.guards_intact() and O.guards_intact()
+    return out
+
+
+def run_rope(q3k, hip, x, B, S, heads, D, cache, start=0, positions=None, offset=0):
+    X, C = Guarded(hip, x, offset=offset), Guarded(hip, cache)
+    Pz = Guarded(hip, positions) if positions is not None else None
+    q3k.rope(X, B, S, heads, D, C, cache.shape[0], start, Pz)
+    hip.synchronize()
+    out = X.get(np.uint16, x.shape)
+    assert X.guards_intact() and C.guards_intact()
+    return out
+
+
+def run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache, start=0, positions=None, eps=EPS, offset=0):
+    Q, K = Guarded(hip, q, offset=offset), Guarded(hip, k, offset=offset)
+    QW, KW, C = Guarded(hip, qw), Guarded(hip, kw), Guarded(hip, cache)
+    Pz = Guarded(hip, positions) if positions is not None else None
+    q3k.qk_norm_rope(Q, K, QW, KW, B, S, Hq, Hkv, D, eps, C, cache.shape[0], start, Pz)
+    hip.synchronize()
+    out = Q.get(np.uint16, q.shape), K.get(np.uint16, k.shape)
+    assert all(b.guards_intact() for b in (Q, K, QW, KW, C))
+    return out
+
+
+# ---------------------------------------------------------------- rms_norm ---
+
+@pytest.mark.parametrize("shape", [(2, 3, 1024), (2, 3, 4, 128)])
+def test_rms_norm_kat(q3k, hip, oracle, shape):
+    announce(f"rms_norm kat {shape}")
+    x, w = kat.rms_input(shape), kat.rms_weight(shape[-1])
+    y = run_rms(q3k, hip, x, w)
+    prim, lo, hi = oracle.rms_norm(x, w, EPS)
+    check_band(oracle, f"rms_norm kat {shape}", y, prim, lo, hi)
+
+
+RMS_CASES = [(16, 1024, 0), (1, 8, 0), (3, 16, 0), (5, 24, 0), (7, 64, 0), (100, 128, 0), (9, 200, 0), (4, 256, 0),
+             (6, 512, 0), (3, 1000, 0), (64, 4096, 0), (17, 5120, 0), (2, 8192, 0), (3, 8200, 0), (5, 257, 0),
+             (7, 1024, 2), (33, 128, 2), (1, 1, 0)]
+
+
+@pytest.mark.parametrize("rows,n,offset", RMS_CASES)
+def test_rms_norm_shapes(q3k, hip, oracle, synth, rows, n, offset):
+    name = f"rms_norm rows={rows} N={n} offset={offset}"
+    announce(name)
+    x = synth.normal_bf16(100, n, (rows, n))
+    w = synth.normal_bf16(101, n, (n,), mean=1.0, std=0.1)
+    y = run_rms(q3k, hip, x, w, offset=offset)
+    prim, lo, hi = oracle.rms_norm(x, w, EPS)
+    check_band(oracle, name, y, prim, lo, hi)
+
+
+def test_rms_norm_config1(q3k, hip, oracle, synth, configs):
+    """x [16, 1024] ~ N(0,1), w ~ N(1, 0.1), eps 1e-6, seed 0."""
+    announce("rms_norm c1")
+    c = configs.CONFIGS["c1"]
+    x = synth.normal_bf16(c.seed, configs.TID_X, (c.seq, c.hidden))
+    w = synth.normal_bf16(c.seed, configs.TID_WF, (c.hidden,), mean=1.0, std=0.1)
+    y = run_rms(q3k, hip, x, w)
+    prim, lo, hi = oracle.rms_norm(x, w, EPS)
+    st = check_band(oracle, "rms_norm c1", y, prim, lo, hi)
+    assert st["ulp_hist"][2] + st["ulp_hist"][3] <= st["ambiguous"]
+
+
+@pytest.mark.parametrize("rows,n,offset", [(16, 1024, 0), (64, 4096, 0), (9, 5120, 0), (3, 8200, 0), (5, 257, 0),
+                                           (11, 1024, 2), (40, 128, 0)])
+def test_add_rms_norm(q3k, hip, oracle, synth, rows, n, offset):
+    name = f"add_rms_norm rows={rows} N={n} offset={offset}"
+    announce(name)
+    h = synth.normal_bf16(102, n, (rows, n))
+    d = synth.normal_bf16(103, n, (rows, n))
+    w = synth.normal_bf16(104, n, (n,), mean=1.0, std=0.1)
+    h_out, y = run_add_rms(q3k, hip, h, d, w, offset=offset)
+    h_ref, prim, lo, hi = oracle.add_rms_norm(h, d, w, EPS)
+    check_exact(name + " residual", h_out, h_ref)
+    check_band(oracle, name, y, prim, lo, hi)
+
+
+# ---------------------------------------------------------------- elementwise -
+
+def test_elementwise_kat(q3k, hip, oracle):
+    announce("elementwise kat")
+    r, d, g, u = kat.elementwise_inputs()
+    check_exact("add kat", run_binary(q3k, hip, "add", r, d), oracle.add_inplace(r, d))
+    prim, lo, hi = oracle.silu_mul(g, u)
+    check_band(oracle, "silu kat", run_binary(q3k, hip, "silu", g, u), prim, lo, hi)
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (8, 0), (9, 0), (1000, 0), (8191, 0), (65536 + 3, 0),
+                                      (1 << 20, 0), (4097, 2), (1 << 16, 2)])
+def test_elementwise_shapes(q3k, hip, oracle, synth, n, offset):
+    name = f"elementwise n={n} offset={offset}"
+    announce(name)
+    a = synth.normal_bf16(105, n, (n,), std=3.0)
+    b = synth.normal_bf16(106, n, (n,))
+    check_exact("add " + name, run_binary(q3k, hip, "add", a, b, offset), oracle.add_inplace(a, b))
+    prim, lo, hi = oracle.silu_mul(a, b)
+    check_band(oracle, "silu " + name, run_binary(q3k, hip, "silu", a, b, offset), prim, lo, hi)
+
+
+def test_silu_extremes(q3k, hip, oracle, synth):
+    announce("silu extremes")
+    vals = np.array([-100.0, -89.0, -88.0, -87.0, -20.0, -1e-30, 0.0, 1e-30, 20.0, 88.0, 100.0, 3.0e38, -3.0e38,
+                     1e-38, -1e-38, -0.0], np.float32)
+    g = synth.f32_to_bf16(np.tile(vals, 9))  # 144 elements: vector body and scalar tail
+    u = np.full(g.shape, 0x3F80, np.uint16)
+    prim, lo, hi = oracle.silu_mul(g, u)
+    check_band(oracle, "silu extremes", run_binary(q3k, hip, "silu", g, u), prim, lo, hi)
+
+
+def test_silu_output_may_alias_input(q3k, hip, oracle, synth):
+    announce("silu in place")
+    g = synth.normal_bf16(107, 0, (4096 + 5,))
+    u = synth.normal_bf16(107, 1, (4096 + 5,))
+    G, U = Guarded(hip, g), Guarded(hip, u)
+    q3k.silu_mul(G, U, G, g.size)
+    hip.synchronize()
+    prim, lo, hi = oracle.silu_mul(g, u)
+    check_band(oracle, "silu in place", G.get(np.uint16, g.shape), prim, lo, hi)
+
+
+# ---------------------------------------------------------------- embedding ---
+
+def test_embedding_kat(q3k, hip, oracle):
+    announce("embedding kat")
+    table, ids = kat.embedding_inputs()
+    check_exact("embedding kat", run_embedding(q3k, hip, ids, table), oracle.embedding(ids, table))
+
+
+@pytest.mark.parametrize("V,H,T,offset", [(1000, 1024, 300, 0), (500, 4096, 77, 0), (300, 5120, 64, 0),
+                                          (50, 8, 9, 0), (64, 12, 33, 0), (100, 1024, 10, 2), (10, 40960, 3, 0)])
+def test_embedding_shapes(q3k, hip, oracle, synth, V, H, T, offset):
+    name = f"embedding V={V} H={H} T={T} offset={offset}"
+    announce(name)
+    table = synth.normal_bf16(108, H, (V, H), std=0.02)
+    ids = synth.token_ids(109, T, (T,), V)
+    ids[:3] = [-1, V, V - 1][:min(3, T)]
+    check_exact(name, run_embedding(q3k, hip, ids, table, offset), oracle.embedding(ids, table))
+
+
+# ---------------------------------------------------------------- rope -------
+
+def test_rope_kat(q3k, hip, oracle):
+    announce("rope kat")
+    B, S, Hq, Hkv, D, P, start = (kat.ROPE_B, kat.ROPE_S, kat.ROPE_HQ, kat.ROPE_HKV, kat.ROPE_D, kat.ROPE_P,
+                                  kat.ROPE_START)
+    cache = q3k.build_rope_cache(P, D, kat.ROPE_THETA)
+    for heads, off in ((Hq, 0), (Hkv, 5)):
+        v = kat.rope_values(B * S * heads * D, off).reshape(B, S, heads * D)
+        prim, lo, hi = oracle.rope(v, B, S, heads, D, cache, start)
+        check_band(oracle, f"rope kat heads={heads}", run_rope(q3k, hip, v, B, S, heads, D, cache, start),
+                   prim, lo, hi)
+    with pytest.raises(IndexError):
+        X, C = Guarded(hip, v), Guarded(hip, cache)
+        q3k.rope(X, B, S, Hkv, D, C, P, P - 1)
+
+
+@pytest.mark.parametrize("B,S,heads,D,start,offset", [(1, 64, 16, 128, 0, 0), (2, 33, 8, 128, 100, 0),
+                                                      (4, 16, 32, 128, 7, 0), (1, 5, 2, 128, 0, 0),
+                                                      (2, 9, 4, 64, 3, 0), (1, 7, 8, 128, 0, 2),
+                                                      (3, 4, 6, 128, 1, 0)])
+def test_rope_shapes(q3k, hip, oracle, synth, B, S, heads, D, start, offset):
+    name = f"rope B={B} S={S} heads={heads} D={D} start={start} offset={offset}"
+    announce(name)
+    cache = q3k.build_rope_cache(start + S + 3, D, 1.0e6)
+    x = synth.normal_bf16(110, heads * S, (B, S, heads * D))
+    prim, lo, hi = oracle.rope(x, B, S, heads, D, cache, start)
+    check_band(oracle, name, run_rope(q3k, hip, x, B, S, heads, D, cache, start, offset=offset), prim, lo, hi)
+
+
+def test_rope_positions_overload(q3k, hip, oracle, synth):
+    announce("rope positions")
+    B, S, heads, D, P = 64, 1, 32, 128, 4096
+    cache = q3k.build_rope_cache(P, D, 1.0e6)
+    x = synth.normal_bf16(111, 0, (B, S, heads * D))
+    pos = synth.uniform_positions(111, 1, B * S, P)
+    pos[:4] = [0, P - 1, P, -5]  # the last two are outside the table: NaN heads
+    prim, lo, hi = oracle.rope(x, B, S, heads, D, cache, positions=pos)
+    got = run_rope(q3k, hip, x, B, S, heads, D, cache, positions=pos)
+    check_band(oracle, "rope positions", got, prim, lo, hi)
+    assert np.all((got[2:4] & 0x7FFF) > 0x7F80)
+
+
+# ---------------------------------------------------------------- qk norm + rope
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,D,start,offset", [(1, 512, 16, 8, 128, 0, 0), (4, 64, 32, 8, 128, 0, 0),
+                                                       (2, 32, 64, 8, 128, 5, 0), (1, 3, 2, 1, 8, 5, 0),
+                                                       (2, 5, 6, 2, 128, 0, 0), (1, 8, 4, 4, 128, 0, 2),
+                                                       (1, 4, 4, 4, 64, 2, 0)])
+def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, offset):
+    name = f"qk_norm_rope B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} start={start} offset={offset}"
+    announce(name)
+    cache = q3k.build_rope_cache(start + S + 1, D, 1.0e6)
+    q = synth.normal_bf16(112, Hq * S, (B, S, Hq * D))
+    k = synth.normal_bf16(113, Hkv * S, (B, S, Hkv * D))
+    qw = synth.normal_bf16(114, D, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(115, D, (D,), mean=1.0, std=0.1)
+    gq, gk = run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache, start, offset=offset)
+    pq, lq, hq = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, cache, start)
+    pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache, start)
+    check_band(oracle, name + " q", gq, pq, lq, hq)
+    check_band(oracle, name + " k", gk, pk, lk, hk)
+
+
+def test_qk_norm_rope_positions_overload(q3k, hip, oracle, synth):
+    announce("qk_norm_rope positions")
+    B, S, Hq, Hkv, D, P = 64, 1, 32, 8, 128, 4096
+    cache = q3k.build_rope_cache(P, D, 1.0e6)
+    q = synth.normal_bf16(116, 0, (B, S, Hq * D))
+    k = synth.normal_bf16(116, 1, (B, S, Hkv * D))
+    qw = synth.normal_bf16(116, 2, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(116, 3, (D,), mean=1.0, std=0.1)
+    pos = synth.uniform_positions(116, 4, B * S, P)
+    pos[5] = P + 10
+    gq, gk = run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache, positions=pos)
+    pq, lq, hq = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, cache, positions=pos)
+    pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache, positions=pos)
+    check_band(oracle, "qknr positions q", gq, pq, lq, hq)
+    check_band(oracle, "qknr positions k", gk, pk, lk, hk)
+    assert np.all((gq[5] & 0x7FFF) > 0x7F80) and np.all((gk[5] & 0x7FFF) > 0x7F80)
+
+
+def test_fused_equals_unfused_on_gpu(q3k, hip, synth):
+    """The fused kernels against the drop-in ops composed in reference order
+    (decoder_layer.cpp:78->88, self_attention.cpp:147-152), both on the GPU."""
+    announce("fused vs unfused")
+    T, H, Hq, Hkv, D = 96, 1024, 16, 8, 128
+    h = synth.normal_bf16(117, 0, (T, H))
+    d = synth.normal_bf16(117, 1, (T, H))
+    w = synth.normal_bf16(117, 2, (H,), mean=1.0, std=0.1)
+    h1, y1 = run_add_rms(q3k, hip, h, d, w)
+    hb = run_binary(q3k, hip, "add", h, d)
+    y2 = run_rms(q3k, hip, hb, w)
+    check_exact("add_rms_norm residual vs add_inplace", h1, hb)
+    check_exact("add_rms_norm vs add_inplace + rms_norm", y1, y2)
+
+    cache = q3k.build_rope_cache(T, D, 1.0e6)
+    q = synth.normal_bf16(117, 3, (1, T, Hq * D))
+    k = synth.normal_bf16(117, 4, (1, T, Hkv * D))
+    qw = synth.normal_bf16(117, 5, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(117, 6, (D,), mean=1.0, std=0.1)
+    fq, fk = run_qknr(q3k, hip, q, k, qw, kw, 1, T, Hq, Hkv, D, cache)
+    nq = run_rms(q3k, hip, q, qw)
+    nk = run_rms(q3k, hip, k, kw)
+    check_exact("qk_norm_rope vs rms_norm + rope (q)", fq, run_rope(q3k, hip, nq, 1, T, Hq, D, cache))
+    check_exact("qk_norm_rope vs rms_norm + rope (k)", fk, run_rope(q3k, hip, nk, 1, T, Hkv, D, cache))

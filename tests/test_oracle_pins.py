@@ -1,0 +1,347 @@
+"""Pins of the CPU oracle (CPU only).
+
+The oracle restates the reference's arithmetic; these tests check it against
+what does not depend on the oracle itself:
+  * the reference tests' known-answer inputs and tolerances (kat.py);
+  * closed forms evaluated in float64 / complex128;
+  * an independent implementation: PyTorch CPU in the Hugging Face Qwen3
+    order (RMSNorm rounds to bf16 before the weight, silu in fp32 then bf16,
+    rotate_half RoPE);
+  * invariants (identity at position 0, scale invariance, norm preservation).
+Where an exact fp32 result of the reference cannot be known (CUDA rsqrtf /
+expf / contraction), a disagreement is only allowed on elements the oracle
+marks ambiguous (lo != hi); everywhere else the primary result must match
+bit for bit.  That is what makes a dropped rounding step or a wrong pair
+index fail here.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kat
+
+
+def t_bf16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).astype(np.int16)).view(torch.bfloat16)
+
+
+def np_bits(t):
+    return t.contiguous().view(torch.int16).numpy().astype(np.uint16)
+
+
+def f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_matches_where_unambiguous(primary, lo, hi, other, name, min_exact=0.995):
+    primary, lo, hi, other = (np.asarray(a).ravel() for a in (primary, lo, hi, other))
+    diff = primary != other
+    ambiguous = lo != hi
+    # Disagreements are allowed only inside the band of ambiguous elements.
+    bad = diff & ~ambiguous
+    assert not bad.any(), f"{name}: {bad.sum()} unambiguous mismatches, first at {np.argmax(bad)}"
+
+    def ordv(b):
+        b = b.astype(np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b)
+
+    inside = (ordv(other) >= ordv(lo)) & (ordv(other) <= ordv(hi))
+    assert inside.all(), f"{name}: independent result outside the band at {np.argmin(inside)}"
+    assert (1.0 - diff.mean()) >= min_exact, f"{name}: only {1 - diff.mean():.5f} exact"
+
+
+# ---------------------------------------------------------------- bf16 --------
+
+def test_bf16_rounding_matches_torch(oracle, synth):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0x3F808000, 0x3F818000, 0x3F80FFFF, 0x7F7FFFFF, 0x00000001, 0x80000000, 0x00008000,
+                         0x7F800000, 0xFF800000, 0x3F7FFFFF], dtype=np.uint32)
+    bits = np.concatenate([bits, specials])
+    x = bits.view(np.float32)
+    finite = np.isfinite(x) | np.isinf(x)
+    ours = np.array([oracle.bf16(float(v)) for v in x[:2000]], dtype=np.uint16)
+    ref = np_bits(torch.from_numpy(x[:2000]).to(torch.bfloat16))
+    keep = finite[:2000]
+    assert np.array_equal(ours[keep], ref[keep])
+    # the numpy generator uses the same rule on the whole sample
+    npr = synth.f32_to_bf16(x)
+    tr = np_bits(torch.from_numpy(x).to(torch.bfloat16))
+    assert np.array_equal(npr[finite], tr[finite])
+    # ties to even, overflow to inf
+    assert oracle.bf16(float(np.uint32(0x3F808000).view(np.float32))) == 0x3F80
+    assert oracle.bf16(float(np.uint32(0x3F818000).view(np.float32))) == 0x3F82
+    assert oracle.bf16(float(np.uint32(0x7F7FFFFF).view(np.float32))) == 0x7F80
+
+
+def test_ulp_distance_and_compare(oracle):
+    assert oracle.ulp_distance(0x3F80, 0x3F81) == 1
+    assert oracle.ulp_distance(0x0000, 0x8000) == 0
+    assert oracle.ulp_distance(0x0001, 0x8001) == 2
+    assert oracle.ulp_distance(0x7FC0, 0x7FC1) == 0
+    assert oracle.ulp_distance(0x7FC0, 0x3F80) > 1000
+    prim = np.array([0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x7FC0], np.uint16)
+    lo = np.array([0x3F80, 0x3F80, 0x3F7F, 0x3F80, 0x7FC0], np.uint16)
+    hi = np.array([0x3F80, 0x3F80, 0x3F81, 0x3F80, 0x7FC0], np.uint16)
+    got = np.array([0x3F81, 0x3F82, 0x3F7E, 0x3F80, 0x7FC0], np.uint16)
+    st = oracle.compare(got, prim, lo, hi)
+    assert st["fail"] == 1 and st["first_fail"] == 1
+    assert st["ambiguous"] == 1
+    assert st["ulp_hist"] == [2, 1, 2, 0]
+
+
+# ---------------------------------------------------------------- embedding ---
+
+def test_embedding_kat(oracle):
+    table, ids = kat.embedding_inputs()
+    out = oracle.embedding(ids, table)
+    assert out.shape == (2, 3, 4)
+    expected = (ids[..., None] * 10 + np.arange(4)).astype(np.float32)
+    assert np.all(np.abs(f32(out) - expected) < 0.001)  # embedding_cuda_test.cpp:204-208
+
+
+def test_embedding_random_and_out_of_range(oracle, synth):
+    table = synth.normal_bf16(11, 0, (97, 24))
+    ids = np.array([0, 96, 5, -1, 97, 2**31 - 1, -(2**31), 40], dtype=np.int32)
+    out = oracle.embedding(ids, table)
+    for t, i in enumerate(ids):
+        if 0 <= i < 97:
+            assert np.array_equal(out[t], table[i])
+        else:
+            assert np.all(out[t] == 0)  # embedding.cu:38-45: +0.0 rows
+
+
+# ---------------------------------------------------------------- add --------
+
+def test_add_matches_fp32_add(oracle, synth):
+    a = synth.normal_bf16(12, 0, (4, 3, 257))
+    b = synth.normal_bf16(12, 1, (4, 3, 257), std=0.5)
+    ours = oracle.add_inplace(a, b)
+    ref = np_bits((t_bf16(a).float() + t_bf16(b).float()).to(torch.bfloat16))
+    assert np.array_equal(ours, ref)
+
+
+def test_add_kat(oracle):
+    r, d, _, _ = kat.elementwise_inputs()
+    out = oracle.add_inplace(r, d)
+    expected = f32(r) + f32(d)  # every KAT sum is exact in bf16
+    assert np.all(np.abs(f32(out) - expected) < 0.001)  # elementwise_cuda_test.cpp:231-234
+
+
+# ---------------------------------------------------------------- rms_norm ---
+
+def hf_rms_norm(x_bits, w_bits, eps):
+    """transformers Qwen3RMSNorm.forward, on the CPU."""
+    hs = t_bf16(x_bits).float()
+    var = hs.pow(2).mean(-1, keepdim=True)
+    hs = hs * torch.rsqrt(var + eps)
+    return np_bits(t_bf16(w_bits) * hs.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 1024), (2, 3, 4, 128)])
+def test_rms_norm_kat(oracle, shape):
+    x = kat.rms_input(shape)
+    w = kat.rms_weight(shape[-1])
+    y, lo, hi = oracle.rms_norm(x, w, 1e-6)
+    xf = f32(x).astype(np.float64).reshape(-1, shape[-1])
+    inv = 1.0 / np.sqrt((xf**2).mean(axis=1, keepdims=True) + 1e-6)
+    expected = (xf * inv * f32(w)).reshape(shape)
+    tol = 0.02 + 0.01 * np.abs(expected)  # rms_norm_cuda_test.cpp:232-235
+    assert np.all(np.abs(f32(y) - expected) <= tol)
+    assert np.all(f32(lo) <= f32(y)) and np.all(f32(y) <= f32(hi))
+
+
+@pytest.mark.parametrize("rows,n", [(64, 1024), (32, 4096), (16, 5120), (512, 128), (8, 257)])
+def test_rms_norm_matches_hf_torch(oracle, synth, rows, n):
+    x = synth.normal_bf16(13, n, (rows, n))
+    w = synth.normal_bf16(13, n + 1, (n,), mean=1.0, std=0.1)
+    y, lo, hi = oracle.rms_norm(x, w, 1e-6)
+    ref = hf_rms_norm(x, w, 1e-6)
+    assert_matches_where_unambiguous(y, lo, hi, ref, f"rms_norm[{rows},{n}]")
+
+
+def test_rms_norm_dropped_rounding_is_detected(oracle, synth):
+    """A restatement that skipped RNE(x * inv) must fail the rule used above."""
+    x = synth.normal_bf16(14, 0, (64, 1024))
+    w = synth.normal_bf16(14, 1, (1024,), mean=1.0, std=0.1)
+    y, lo, hi = oracle.rms_norm(x, w, 1e-6)
+    hs = t_bf16(x).float()
+    hs = hs * torch.rsqrt(hs.pow(2).mean(-1, keepdim=True) + 1e-6)
+    wrong = np_bits((t_bf16(w).float() * hs).to(torch.bfloat16))  # one rounding only
+    with pytest.raises(AssertionError):
+        assert_matches_where_unambiguous(y, lo, hi, wrong, "planted")
+
+
+def test_rms_norm_constant_row_closed_form(oracle):
+    n = 1024
+    x = np.full((3, n), 0x3F00, np.uint16)  # 0.5
+    w = np.full((n,), 0x3F80, np.uint16)    # 1.0
+    y, _, _ = oracle.rms_norm(x, w, 1e-6)
+    # inv = 1/sqrt(0.25 + 1e-6) = 1.999996; 0.5 * inv rounds to 1.0 in bf16
+    assert np.all(y == 0x3F80)
+
+
+def test_rms_norm_scale_invariance(oracle, synth):
+    x = synth.normal_bf16(15, 0, (8, 4096))
+    w = synth.normal_bf16(15, 1, (4096,), mean=1.0, std=0.1)
+    x2 = (x.astype(np.uint32) + (1 << 7)).astype(np.uint16)  # exponent + 1: exactly 2x (normal values)
+    assert np.allclose(f32(x2)[np.abs(f32(x)) > 1e-30], 2 * f32(x)[np.abs(f32(x)) > 1e-30])
+    y1, _, _ = oracle.rms_norm(x, w, 1e-30)
+    y2, _, _ = oracle.rms_norm(x2, w, 1e-30)
+    assert np.array_equal(y1, y2)
+
+
+def test_rms_norm_packed_heads_equal_rows(oracle, synth):
+    q = synth.normal_bf16(16, 0, (5, 7, 4 * 128))
+    w = synth.normal_bf16(16, 1, (128,), mean=1.0, std=0.1)
+    a, _, _ = oracle.rms_norm(q, w, 1e-6)
+    b, _, _ = oracle.rms_norm(q.reshape(-1, 128), w, 1e-6)
+    assert np.array_equal(a.reshape(-1), b.reshape(-1))
+
+
+def test_add_rms_norm_is_composition(oracle, synth):
+    h = synth.normal_bf16(17, 0, (33, 1024))
+    d = synth.normal_bf16(17, 1, (33, 1024))
+    w = synth.normal_bf16(17, 2, (1024,), mean=1.0, std=0.1)
+    h2, y, lo, hi = oracle.add_rms_norm(h, d, w, 1e-6)
+    assert np.array_equal(h2, oracle.add_inplace(h, d))
+    y_ref, lo_ref, hi_ref = oracle.rms_norm(h2, w, 1e-6)
+    assert np.array_equal(y, y_ref) and np.array_equal(lo, lo_ref) and np.array_equal(hi, hi_ref)
+    # decoder_layer.cpp:78->88 in torch: add in bf16, then the HF norm of the rounded sum
+    hs = np_bits((t_bf16(h).float() + t_bf16(d).float()).to(torch.bfloat16))
+    assert_matches_where_unambiguous(y, lo, hi, hf_rms_norm(hs, w, 1e-6), "add_rms_norm")
+
+
+# ---------------------------------------------------------------- silu -------
+
+def test_silu_mul_matches_hf_torch(oracle, synth):
+    g = synth.normal_bf16(18, 0, (512, 3072))
+    u = synth.normal_bf16(18, 1, (512, 3072))
+    out, lo, hi = oracle.silu_mul(g, u)
+    act = torch.nn.functional.silu(t_bf16(g).float()).to(torch.bfloat16)  # silu(gate) in bf16
+    ref = np_bits(act * t_bf16(u))
+    assert_matches_where_unambiguous(out, lo, hi, ref, "silu_mul")
+
+
+def test_silu_mul_closed_form(oracle, synth):
+    g = synth.normal_bf16(19, 0, (100_000,), std=4.0)
+    u = synth.normal_bf16(19, 1, (100_000,))
+    out, lo, hi = oracle.silu_mul(g, u)
+    gd = f32(g).astype(np.float64)
+    s = gd / (1.0 + np.exp(-gd))
+    n = synth.f32_to_bf16(s.astype(np.float32))
+    exact = synth.f32_to_bf16(f32(n) * f32(u))
+    assert_matches_where_unambiguous(out, lo, hi, exact, "silu closed form")
+
+
+def test_silu_mul_kat_and_extremes(oracle):
+    _, _, g, u = kat.elementwise_inputs()
+    out, _, _ = oracle.silu_mul(g, u)
+    gf, uf = f32(g).astype(np.float64), f32(u).astype(np.float64)
+    expected = gf / (1 + np.exp(-gf)) * uf
+    assert np.all(np.abs(f32(out) - expected) <= 0.02 + 0.01 * np.abs(expected))  # :294-303
+    # exp(-g) overflows fp32 for g < -88.7: silu is a signed zero, as expf gives inf
+    g2 = kat.bf(np.array([-100.0, -89.0, 100.0, 0.0], np.float32))
+    u2 = kat.bf(np.array([1.0, 1.0, 1.0, 1.0], np.float32))
+    o2, _, _ = oracle.silu_mul(g2, u2)
+    assert list(f32(o2)) == [0.0, 0.0, 100.0, 0.0]
+
+
+# ---------------------------------------------------------------- rope -------
+
+def test_rope_cache_closed_form(oracle):
+    P, D, theta = 64, 128, 1.0e6
+    cache = oracle.build_rope_cache(P, D, theta)
+    p = np.arange(P)[:, None].astype(np.float64)
+    i = np.arange(D // 2)[None, :].astype(np.float64)
+    ang = p * theta ** (-(2.0 * i) / D)
+    assert np.array_equal(cache[..., 0], np.cos(ang).astype(np.float32))
+    assert np.array_equal(cache[..., 1], np.sin(ang).astype(np.float32))
+    assert np.all(cache[0, :, 0] == 1.0) and np.all(cache[0, :, 1] == 0.0)
+
+
+def hf_rope(x_bits, heads, D, cache, pos):
+    """transformers apply_rotary_pos_emb with rotate_half, fp32 table, on the CPU."""
+    x = t_bf16(x_bits).float().reshape(len(pos), heads, D)
+    cs = torch.from_numpy(cache[pos])  # [T, D/2, 2]
+    cos = torch.cat([cs[..., 0], cs[..., 0]], -1)[:, None, :]
+    sin = torch.cat([cs[..., 1], cs[..., 1]], -1)[:, None, :]
+    rot = torch.cat([-x[..., D // 2:], x[..., : D // 2]], -1)
+    return np_bits((x * cos + rot * sin).to(torch.bfloat16)).reshape(x_bits.shape)
+
+
+def test_rope_kat(oracle):
+    B, S, Hq, Hkv, D, P, start, theta = (kat.ROPE_B, kat.ROPE_S, kat.ROPE_HQ, kat.ROPE_HKV, kat.ROPE_D, kat.ROPE_P,
+                                         kat.ROPE_START, kat.ROPE_THETA)
+    cache = oracle.build_rope_cache(P, D, theta)
+    for heads, off in ((Hq, 0), (Hkv, 5)):
+        v = kat.rope_values(B * S * heads * D, off).reshape(B, S, heads * D)
+        out, _, _ = oracle.rope(v, B, S, heads, D, cache, start)
+        x = f32(v).astype(np.float64).reshape(B, S, heads, D)
+        z = x[..., : D // 2] + 1j * x[..., D // 2:]
+        pos = start + np.arange(S)
+        ang = pos[:, None] * theta ** (-(2.0 * np.arange(D // 2)) / D)
+        r = z * np.exp(1j * ang)[None, :, None, :]
+        expected = np.concatenate([r.real, r.imag], -1).reshape(B, S, heads * D)
+        assert np.all(np.abs(f32(out) - expected) <= 0.03)  # rope_cuda_test.cpp:325-335
+    with pytest.raises(ValueError):
+        oracle.rope(v, B, S, Hkv, D, cache, P - 1)  # rope_cuda_test.cpp:337-358
+
+
+@pytest.mark.parametrize("heads,S,start", [(16, 64, 0), (8, 33, 100), (32, 8, 4000)])
+def test_rope_matches_rotate_half(oracle, synth, heads, S, start):
+    D, P = 128, 4096 + 64
+    cache = oracle.build_rope_cache(P, D, 1.0e6)
+    x = synth.normal_bf16(20, heads, (2, S, heads * D))
+    out, lo, hi = oracle.rope(x, 2, S, heads, D, cache, start)
+    pos = np.tile(start + np.arange(S), 2)
+    ref = hf_rope(x.reshape(2 * S, heads * D), heads, D, cache, pos).reshape(x.shape)
+    assert_matches_where_unambiguous(out, lo, hi, ref, "rope")
+
+
+def test_rope_complex_closed_form_and_identity(oracle, synth):
+    D, heads, S = 128, 4, 40
+    cache = oracle.build_rope_cache(64, D, 1.0e6)
+    x = synth.normal_bf16(21, 0, (1, S, heads * D))
+    out, lo, hi = oracle.rope(x, 1, S, heads, D, cache, 0)
+    # position 0 is the identity: cos = 1, sin = 0 exactly
+    assert np.array_equal(out[0, 0], x[0, 0])
+    xf = f32(x).astype(np.float64).reshape(S, heads, D)
+    c = cache[:S, :, 0].astype(np.float64)[:, None, :]
+    s = cache[:S, :, 1].astype(np.float64)[:, None, :]
+    z = (xf[..., : D // 2] + 1j * xf[..., D // 2:]) * (c + 1j * s)
+    exact = np.concatenate([z.real, z.imag], -1).astype(np.float32).reshape(x.shape)
+    assert_matches_where_unambiguous(out, lo, hi, synth.f32_to_bf16(exact), "rope complex")
+    # rotation preserves each pair's norm up to bf16 rounding
+    a = f32(out).astype(np.float64).reshape(S, heads, D)
+    n0 = xf[..., : D // 2] ** 2 + xf[..., D // 2:] ** 2
+    n1 = a[..., : D // 2] ** 2 + a[..., D // 2:] ** 2
+    assert np.allclose(n1, n0, rtol=2e-2, atol=1e-6)
+
+
+def test_rope_positions_and_out_of_range(oracle, synth):
+    D, heads = 128, 8
+    cache = oracle.build_rope_cache(100, D, 1.0e6)
+    x = synth.normal_bf16(22, 0, (3, 1, heads * D))
+    pos = np.array([7, 99, 100], np.int32)
+    out, _, _ = oracle.rope(x, 3, 1, heads, D, cache, positions=pos)
+    for b in range(2):
+        one, _, _ = oracle.rope(x[b:b + 1], 1, 1, heads, D, cache, start=int(pos[b]))
+        assert np.array_equal(out[b], one[0])
+    assert np.all(out[2] == 0x7FC0)  # position outside the table: NaN row
+
+
+def test_qk_norm_rope_is_composition(oracle, synth):
+    D, heads, B, S = 128, 8, 2, 24
+    cache = oracle.build_rope_cache(64, D, 1.0e6)
+    x = synth.normal_bf16(23, 0, (B, S, heads * D))
+    w = synth.normal_bf16(23, 1, (D,), mean=1.0, std=0.1)
+    fused, lo, hi = oracle.qk_norm_rope(x, w, B, S, heads, D, 1e-6, cache, start=3)
+    normed, _, _ = oracle.rms_norm(x, w, 1e-6)
+    roped, _, _ = oracle.rope(normed, B, S, heads, D, cache, start=3)
+    assert np.array_equal(fused, roped)
+    # self_attention.cpp:147-152 in torch: HF q_norm, then rotate_half RoPE
+    normed_t = hf_rms_norm(x.reshape(-1, D), w, 1e-6).reshape(B * S, heads * D)
+    pos = np.tile(3 + np.arange(S), B)
+    ref = hf_rope(normed_t, heads, D, cache, pos).reshape(x.shape)
+    assert_matches_where_unambiguous(fused, lo, hi, ref, "qk_norm_rope", min_exact=0.99)
