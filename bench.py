@@ -11,12 +11,13 @@ synthetic input at BASELINE config 4 (Qwen3-8B prefill, T = 8192 tokens as
   add_rms_norm  h2 += d2; y2 = rmsnorm(h2)     [8192, 4096]   MLP residual + next layer's input norm
   silu_mul      o = silu(g) * u                [8192, 12288]
 
-Every tensor of a step is distinct and the steps rotate over two full input
-sets (2 x 1.31 GB, far above the 256 MB Infinity Cache), so each launch reads
-its inputs from HBM.  ``value`` is the chain's algorithmic bytes (each
+Every tensor of a step is distinct and the steps rotate over six full input
+sets (6 x 1.31 GB; the smallest per-op cycle, 6 x 80 MB of Q/K, is still far
+above the 256 MB Infinity Cache), so each launch reads its inputs from HBM.  ``value`` is the chain's algorithmic bytes (each
 compulsory byte once) divided by the measured time per step, inputs already
-resident in HBM.  Per-kernel durations come from HIP events around every
-launch inside the same timed region.
+resident in HBM.  Per-kernel durations come from back-to-back launches of
+each kernel alone (rotating over the same input sets) between one pair of
+HIP events.
 
 Also reported (not part of ``value``): the embedding gather and the final
 RMSNorm at config 4, the same chain built from the unfused drop-in ops in
@@ -53,28 +54,12 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c4")
-    ap.add_argument("--sets", type=int, default=2, help="rotating input sets")
+    ap.add_argument("--sets", type=int, default=6,
+                    help="rotating input sets (6: even the smallest per-op cycle, 6 x 80 MB, exceeds the 256 MB cache)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extras", action="store_true", help="chain only (no embedding/final-norm/unfused/copy)")
     return ap.parse_args()
-
-
-class Timer:
-    """Per-launch HIP event pairs recorded on the launch stream."""
-
-    def __init__(self, hip, stream, names, steps):
-        self.hip, self.stream = hip, stream
-        self.events = {n: [(hip.Event(), hip.Event()) for _ in range(steps)] for n in names}
-
-    def run(self, name, i, fn):
-        a, b = self.events[name][i]
-        a.record(self.stream)
-        fn()
-        b.record(self.stream)
-
-    def mean_ms(self, name):
-        return float(np.mean([a.elapsed_ms(b) for a, b in self.events[name]]))
 
 
 def make_chain_set(hip, synth, configs, c, q3k, seed_shift=0):
@@ -139,27 +124,34 @@ def unfused_ops(q3k, c, b, stream):
     ]
 
 
-def time_ops(hip, stream, sets, make_ops, steps, warmup):
-    """Warm up, then time `steps` passes (rotating over `sets`) with per-op events.
-    Returns (ms per step, {op: mean ms})."""
-    names = [n for n, _ in make_ops(sets[0])]
+def time_chain(hip, stream, sets, make_ops, steps, warmup):
+    """Warm up, then time `steps` passes of the op list (rotating over the
+    input sets) between one pair of events; returns ms per pass."""
     per_set = [make_ops(s) for s in sets]
     for i in range(warmup):
         for _, fn in per_set[i % len(sets)]:
             fn()
-    stream.synchronize()
-    timer = Timer(hip, stream, names, steps)
     start, stop = hip.Event(), hip.Event()
     hip.synchronize()
     start.record(stream)
     for i in range(steps):
-        for n, fn in per_set[i % len(sets)]:
-            timer.run(n, i, fn)
+        for _, fn in per_set[i % len(sets)]:
+            fn()
     stop.record(stream)
     stop.synchronize()
     hip.synchronize()
-    total = start.elapsed_ms(stop)
-    return total / steps, {n: timer.mean_ms(n) for n in names}
+    return start.elapsed_ms(stop) / steps
+
+
+def time_each_op(hip, stream, sets, make_ops, reps, warmup=2):
+    """Per-op duration: `reps` back-to-back launches of one op (rotating over
+    the input sets, so every launch reads from HBM) between one pair of
+    events; returns {op: ms per launch}."""
+    per_set = [make_ops(s) for s in sets]
+    out = {}
+    for k, (name, _) in enumerate(per_set[0]):
+        out[name] = time_chain(hip, stream, sets, lambda s, k=k: [make_ops(s)[k]], reps, warmup)
+    return out
 
 
 def read_traffic(kernel_key):
@@ -256,7 +248,9 @@ def main():
     sets = [base] + [clone_set(hip, base) for _ in range(max(1, args.sets) - 1)]
     print(f"[bench] timing chain: {args.warmup} warmup + {args.steps} steps over {len(sets)} sets",
           file=sys.stderr, flush=True)
-    ms_step, per_op = time_ops(hip, stream, sets, lambda b: chain_ops(q3k, c, b, stream), args.steps, args.warmup)
+    make_chain = lambda b: chain_ops(q3k, c, b, stream)  # noqa: E731
+    ms_step = time_chain(hip, stream, sets, make_chain, args.steps, args.warmup)
+    per_op = time_each_op(hip, stream, sets, make_chain, args.steps)
 
     T, H, I = c.tokens, c.hidden, c.inter
     U = c.distinct_positions()
@@ -284,23 +278,23 @@ def main():
     extras = {}
     if not args.no_extras:
         print("[bench] timing unfused chain", file=sys.stderr, flush=True)
-        ms_unfused, per_unfused = time_ops(hip, stream, sets, lambda b: unfused_ops(q3k, c, b, stream),
-                                           max(5, args.steps // 2), 3)
+        make_unfused = lambda b: unfused_ops(q3k, c, b, stream)  # noqa: E731
+        ms_unfused = time_chain(hip, stream, sets, make_unfused, max(5, args.steps // 2), 3)
+        per_unfused = time_each_op(hip, stream, sets, make_unfused, max(5, args.steps // 2))
         extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5),
                                    "per_op_ms": {k: round(v, 5) for k, v in per_unfused.items()},
                                    "fused_speedup": round(ms_unfused / ms_step, 3)}
         # final RMSNorm (model.cpp:146) at config 4, reading y1 of the rotating sets
-        fn_sets = sets
-        ms_rn, per_rn = time_ops(hip, stream, fn_sets, lambda b: [
+        ms_rn = time_chain(hip, stream, sets, lambda b: [
             ("rms_norm", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream))],
             max(10, args.steps), 3)
         rb = configs.bytes_rms_norm(T, H)
-        extras["rms_norm_final"] = {"ms": round(per_rn["rms_norm"], 5), "bytes": rb,
-                                    "GB/s": round(rb / (per_rn["rms_norm"] * 1e-3) / 1e9, 1)}
+        extras["rms_norm_final"] = {"ms": round(ms_rn, 5), "bytes": rb,
+                                    "GB/s": round(rb / (ms_rn * 1e-3) / 1e9, 1)}
         # copy ceiling: 1 GiB, 128-bit loads and stores
         nb = 1 << 30
         src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
-        ms_cp, _ = time_ops(hip, stream, [0], lambda _: [("copy", lambda: q3k.bench_copy(src, dst, nb, stream))], 10, 2)
+        ms_cp = time_chain(hip, stream, [0], lambda _: [("copy", lambda: q3k.bench_copy(src, dst, nb, stream))], 10, 2)
         extras["copy_ceiling_GB/s"] = round(2 * nb / (ms_cp * 1e-3) / 1e9, 1)
         src.free()
         dst.free()
@@ -313,7 +307,7 @@ def main():
                 synth.normal_bf16(c.seed, configs.TID_TABLE, (configs.VOCAB, H)))
             ids = hip.DeviceBuffer.from_array(synth.token_ids(c.seed, configs.TID_IDS, (T,), configs.VOCAB))
             out = hip.DeviceBuffer(T * H * 2)
-            ms_e, _ = time_ops(hip, stream, [0], lambda _: [
+            ms_e = time_chain(hip, stream, [0], lambda _: [
                 ("embedding", lambda: q3k.embedding(ids, T, table, configs.VOCAB, H, out, stream))], 20, 3)
             eb = configs.bytes_embedding(T, H)
             extras["embedding"] = {"ms": round(ms_e, 5), "bytes": eb, "GB/s": round(eb / (ms_e * 1e-3) / 1e9, 1)}

@@ -14,7 +14,9 @@ namespace q3k
     {
         constexpr int kTokensPerBlock = kBlock / kWave;
         constexpr int kVpt = 8;
+        constexpr int kNtm = 0;  // measured: plain loads/stores are faster for the random-row gather
 
+        template <int NTM>
         __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(
             const int32_t *__restrict__ ids, int64_t tokens,
             const Vec8 *__restrict__ table, int64_t vocab, int64_t nvec,
@@ -30,7 +32,7 @@ namespace q3k
             {
                 const Vec8 zero = {{0u, 0u, 0u, 0u}};
                 for (int64_t j = lane; j < nvec; j += kWave)
-                    dst[j] = zero;
+                    store8<nt_store(NTM)>(dst + j, zero);
                 return;
             }
             const Vec8 *src = table + static_cast<int64_t>(id) * nvec;
@@ -42,14 +44,14 @@ namespace q3k
                 {
                     const int64_t j = j0 + lane + i * kWave;
                     if (j < nvec)
-                        v[i] = src[j];
+                        v[i] = load8<nt_load(NTM)>(src + j);
                 }
 #pragma unroll
                 for (int i = 0; i < kVpt; ++i)
                 {
                     const int64_t j = j0 + lane + i * kWave;
                     if (j < nvec)
-                        dst[j] = v[i];
+                        store8<nt_store(NTM)>(dst + j, v[i]);
                 }
             }
         }
@@ -91,7 +93,7 @@ extern "C" int q3k_embedding_bf16(const int32_t *ids, int64_t T, const uint16_t 
     const int64_t blocks = (T + kTokensPerBlock - 1) / kTokensPerBlock;
     if (H % 8 == 0 && aligned16(table) && aligned16(out) && blocks < (int64_t{1} << 31))
     {
-        embedding_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
+        embedding_vec_kernel<kNtm><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
             ids, T, reinterpret_cast<const Vec8 *>(table), V, H / 8, reinterpret_cast<Vec8 *>(out));
     }
     else

@@ -1,21 +1,23 @@
 // RMSNorm and fused residual-add + RMSNorm for gfx950.
 //
-// Fast path (N % 8 == 0, N <= 8192, 16-byte aligned pointers): a group of G
-// lanes owns one row and keeps it in registers, so x (and the residual
-// delta) is read from HBM exactly once.  Each lane holds VPT 128-bit
-// vectors (8 bf16 each); vector j of a row sits in lane j % G, slot j / G, so
-// every load instruction of a group reads G * 16 contiguous bytes.  The row
-// sum of squares is reduced across the group with DPP (G <= 16) or
-// cross-lane shuffles, with no LDS and no barrier.  G = 64 is one wave per
-// row (hidden rows of 1024..8192); G = 16 packs four head rows of 128 into a
-// wave (per-head Q/K norm).
+// Fast path (N % 8 == 0, N <= 16384, 16-byte aligned pointers): each row is
+// held in registers between its load and its stores, so x (and the residual
+// delta) is read from HBM exactly once.  Rows are split into 128-bit vectors
+// (8 bf16); vector j sits in thread j % P, slot j / P of the P threads that
+// own the row, so every load instruction of a wave covers 1 KiB of
+// contiguous memory.  Narrow rows (<= 256 elements, e.g. per-head Q/K norm
+// over 128) give each row an aligned group of lanes and reduce the sum of
+// squares with DPP inside the wave; rows up to 1024 elements use one wave;
+// wider rows (hidden 2048 .. 16384) use one block of up to eight waves per
+// row whose wave sums meet in LDS behind one barrier.  Stores are
+// non-temporal.  The mapping per width was chosen by measurement on MI355X.
 //
 // Generic path (any N, any alignment): one 256-thread block per row, scalar
 // loads, two passes over the row (reference structure, wave64 reduction).
 //
 // Arithmetic follows src/ops/rms_norm.cu:82-121 and
 // src/ops/elementwise.cu:28-35: fp32 sum of squares, mean = sum / N,
-// inv = 1/sqrt(mean + eps), y = RNE(RNE(x * inv) * w); the fused form adds
+// inv = rsqrt(mean + eps), y = RNE(RNE(x * inv) * w); the fused form adds
 // h = RNE(h + d) first and normalises the rounded h.
 #include "q3k_common.hpp"
 
@@ -23,11 +25,34 @@ namespace q3k
 {
     namespace
     {
-        template <int G, int VPT, bool ADD>
+        // Normalise the row slice held by this thread: h = RNE(h + d) (ADD),
+        // then the partial sum of squares of the rounded values.
+        template <int VPT, bool ADD>
+        __device__ __forceinline__ float add_and_square(Vec8 (&x)[VPT], const Vec8 (&dv)[VPT], const bool (&live)[VPT])
+        {
+            float partial = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+            {
+                if (!live[i])
+                    continue;
+                if constexpr (ADD)
+                {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        x[i].d[k] = pack_rne(bf_lo(x[i].d[k]) + bf_lo(dv[i].d[k]), bf_hi(x[i].d[k]) + bf_hi(dv[i].d[k]));
+                }
+                partial += sum_sq8(x[i]);
+            }
+            return partial;
+        }
+
+        // Group of G lanes per row (G <= 64), VPT vectors per lane.
+        template <int G, int VPT, bool ADD, int NTM>
         __global__ __launch_bounds__(kBlock) void rms_rows_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
-            int64_t rows, int nvec, float n_float, float eps)
+            int64_t rows, int nvec, float inv_n, float eps)
         {
             constexpr int kRowsPerBlock = kBlock / G;
             const int lane = threadIdx.x % G;
@@ -41,59 +66,92 @@ namespace q3k
             Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row_offset;
 
             // Issue every load of the row (and the weights) before any use.
-            Vec8 x[VPT];
-            Vec8 dv[VPT];
-            Vec8 wv[VPT];
+            Vec8 x[VPT], dv[VPT], wv[VPT];
+            bool live[VPT];
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
             {
                 const int j = lane + i * G;
-                if (j < nvec)
+                live[i] = j < nvec;
+                if (live[i])
                 {
-                    x[i] = hrow[j];
+                    x[i] = load8<nt_load(NTM)>(hrow + j);
                     if constexpr (ADD)
-                        dv[i] = reinterpret_cast<const Vec8 *>(d)[row_offset + j];
+                        dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
                     wv[i] = wvec[j];
                 }
             }
-
+            const float partial = add_and_square<VPT, ADD>(x, dv, live);
             if constexpr (ADD)
             {
 #pragma unroll
                 for (int i = 0; i < VPT; ++i)
-                {
-                    const int j = lane + i * G;
-                    if (j < nvec)
-                    {
-                        Vec8 s;
+                    if (live[i])
+                        store8<nt_store(NTM)>(hrow + lane + i * G, x[i]);
+            }
+            const float inv = inverse_rms(group_sum<G>(partial), inv_n, eps);
 #pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            s.d[k] = pack_rne(bf_lo(x[i].d[k]) + bf_lo(dv[i].d[k]),
-                                              bf_hi(x[i].d[k]) + bf_hi(dv[i].d[k]));
-                        x[i] = s;
-                        hrow[j] = s;
-                    }
+            for (int i = 0; i < VPT; ++i)
+                if (live[i])
+                    store8<nt_store(NTM)>(yrow + lane + i * G, norm_scale8(x[i], wv[i], inv));
+        }
+
+        // WPR waves per row (one row per block), VPT vectors per lane; the
+        // wave sums meet in LDS behind one barrier.
+        template <int WPR, int VPT, bool ADD, int NTM>
+        __global__ __launch_bounds__(WPR * kWave) void rms_block_kernel(
+            uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
+            const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
+            int64_t rows, int nvec, float inv_n, float eps)
+        {
+            constexpr int kThreads = WPR * kWave;
+            __shared__ float wave_sums[WPR];
+            const int t = threadIdx.x;
+            const int64_t row = blockIdx.x;
+            const int64_t row_offset = row * static_cast<int64_t>(nvec);
+            Vec8 *hrow = reinterpret_cast<Vec8 *>(h) + row_offset;
+            const Vec8 *wvec = reinterpret_cast<const Vec8 *>(w);
+            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row_offset;
+
+            Vec8 x[VPT], dv[VPT], wv[VPT];
+            bool live[VPT];
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+            {
+                const int j = t + i * kThreads;
+                live[i] = j < nvec;
+                if (live[i])
+                {
+                    x[i] = load8<nt_load(NTM)>(hrow + j);
+                    if constexpr (ADD)
+                        dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
+                    wv[i] = wvec[j];
                 }
             }
-
-            float partial = 0.0f;
+            const float partial = add_and_square<VPT, ADD>(x, dv, live);
+            if constexpr (ADD)
+            {
+#pragma unroll
+                for (int i = 0; i < VPT; ++i)
+                    if (live[i])
+                        store8<nt_store(NTM)>(hrow + t + i * kThreads, x[i]);
+            }
+            float total = group_sum<kWave>(partial);
+            if constexpr (WPR > 1)
+            {
+                if (t % kWave == 0)
+                    wave_sums[t / kWave] = total;
+                __syncthreads();
+                total = 0.0f;
+#pragma unroll
+                for (int k = 0; k < WPR; ++k)
+                    total += wave_sums[k];
+            }
+            const float inv = inverse_rms(total, inv_n, eps);
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
-            {
-                const int j = lane + i * G;
-                if (j < nvec)
-                    partial += sum_sq8(x[i]);
-            }
-            const float total = group_sum<G>(partial);
-            const float inv = inverse_rms(total, n_float, eps);
-
-#pragma unroll
-            for (int i = 0; i < VPT; ++i)
-            {
-                const int j = lane + i * G;
-                if (j < nvec)
-                    yrow[j] = norm_scale8(x[i], wv[i], inv);
-            }
+                if (live[i])
+                    store8<nt_store(NTM)>(yrow + t + i * kThreads, norm_scale8(x[i], wv[i], inv));
         }
 
         // Block-wide sum for the generic kernel: wave sums through LDS, then
@@ -119,7 +177,7 @@ namespace q3k
             int64_t rows, int64_t n, float eps)
         {
             __shared__ float scratch[kBlock / kWave];
-            const float n_float = static_cast<float>(n);
+            const float inv_n = 1.0f / static_cast<float>(n);
             for (int64_t row = blockIdx.x; row < rows; row += gridDim.x)
             {
                 uint16_t *hr = h + row * n;
@@ -137,7 +195,7 @@ namespace q3k
                     }
                     partial += v * v;
                 }
-                const float inv = inverse_rms(block_sum(partial, scratch), n_float, eps);
+                const float inv = inverse_rms(block_sum(partial, scratch), inv_n, eps);
                 for (int64_t c = threadIdx.x; c < n; c += blockDim.x)
                 {
                     const float nrm = bf_to_f(f_to_bf(bf_to_f(hr[c]) * inv));
@@ -146,61 +204,85 @@ namespace q3k
             }
         }
 
+        // Non-temporal stores, plain loads: the fastest mode measured on MI355X
+        // for every row width of the model (1024 .. 8192), fused or not.
+        constexpr int kNtmRows = 2;
+
         template <int G, int VPT, bool ADD>
         void launch_rows(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                         int64_t rows, int nvec, float n_float, float eps, hipStream_t stream)
+                         int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
         {
             constexpr int kRowsPerBlock = kBlock / G;
             const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-            rms_rows_kernel<G, VPT, ADD><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
-                h, d, w, y, rows, nvec, n_float, eps);
+            rms_rows_kernel<G, VPT, ADD, kNtmRows><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
+                h, d, w, y, rows, nvec, inv_n, eps);
         }
 
+        template <int WPR, int VPT, bool ADD>
+        void launch_block(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
+                          int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
+        {
+            rms_block_kernel<WPR, VPT, ADD, kNtmRows><<<dim3(static_cast<unsigned>(rows)), dim3(WPR * kWave), 0, stream>>>(
+                h, d, w, y, rows, nvec, inv_n, eps);
+        }
+
+        template <int VPT, bool ADD>
+        bool launch_block_waves(int waves, uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
+                                int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
+        {
+            switch (waves)
+            {
+            case 1: launch_block<1, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 2: launch_block<2, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 3: launch_block<3, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 4: launch_block<4, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 5: launch_block<5, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 6: launch_block<6, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 7: launch_block<7, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 8: launch_block<8, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            default: return false;
+            }
+        }
+
+        // Row-to-lane mapping by row width, in 128-bit vectors (measured on MI355X):
+        //   nvec <= 32:   a group of pow2 >= nvec lanes per row, several rows per wave
+        //                 (per-head norms, 128 elements = 16 lanes);
+        //   nvec <= 128:  one wave per row, 1-2 vectors per lane (hidden 1024);
+        //   nvec <= 2048: one row per block of up to 8 waves; one vector per lane
+        //                 for the fused add when nvec <= 512 (hidden <= 4096),
+        //                 else two (four beyond 8192 elements).
         template <bool ADD>
         bool launch_fast(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
                          int64_t rows, int64_t n, float eps, hipStream_t stream)
         {
             const int nvec = static_cast<int>(n / 8);
-            const float nf = static_cast<float>(n);
+            const float inv_n = 1.0f / static_cast<float>(n);
             if (nvec <= 1)
-                launch_rows<1, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<1, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
             else if (nvec <= 2)
-                launch_rows<2, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<2, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
             else if (nvec <= 4)
-                launch_rows<4, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<4, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
             else if (nvec <= 8)
-                launch_rows<8, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<8, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
             else if (nvec <= 16)
-                launch_rows<16, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<16, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
             else if (nvec <= 32)
-                launch_rows<32, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream);
+                launch_rows<32, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+            else if (nvec <= 64)
+                launch_rows<64, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+            else if (nvec <= 128)
+                launch_rows<64, 2, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+            else if (ADD && nvec <= 512)
+                return launch_block_waves<1, ADD>((nvec + 63) / 64, h, d, w, y, rows, nvec, inv_n, eps, stream);
+            else if (nvec <= 1024)
+                return launch_block_waves<2, ADD>((nvec + 127) / 128, h, d, w, y, rows, nvec, inv_n, eps, stream);
             else
-            {
-                switch ((nvec + kWave - 1) / kWave)
-                {
-                case 1: launch_rows<64, 1, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 2: launch_rows<64, 2, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 3: launch_rows<64, 3, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 4: launch_rows<64, 4, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 5: launch_rows<64, 5, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 6: launch_rows<64, 6, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 7: launch_rows<64, 7, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 8: launch_rows<64, 8, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 9: launch_rows<64, 9, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 10: launch_rows<64, 10, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 11: launch_rows<64, 11, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 12: launch_rows<64, 12, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 13: launch_rows<64, 13, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 14: launch_rows<64, 14, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 15: launch_rows<64, 15, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                case 16: launch_rows<64, 16, ADD>(h, d, w, y, rows, nvec, nf, eps, stream); break;
-                default: return false;
-                }
-            }
+                return launch_block_waves<4, ADD>((nvec + 255) / 256, h, d, w, y, rows, nvec, inv_n, eps, stream);
             return true;
         }
 
-        constexpr int64_t kMaxFastN = 16 * kWave * 8; // 8192 elements per row
+        constexpr int64_t kMaxFastN = 8 * kWave * 4 * 8; // 16384 elements per row
         constexpr int64_t kMaxGenericBlocks = 1 << 20;
 
         template <bool ADD>
@@ -208,7 +290,7 @@ namespace q3k
                          int64_t rows, int64_t n, float eps, hipStream_t stream, const char *name)
         {
             const bool fast = (n % 8 == 0) && n <= kMaxFastN && aligned16(h) && aligned16(w) && aligned16(y) &&
-                              (!ADD || aligned16(d)) && rows <= (int64_t{1} << 31);
+                              (!ADD || aligned16(d)) && rows < (int64_t{1} << 31);
             if (!(fast && launch_fast<ADD>(h, d, w, y, rows, n, eps, stream)))
             {
                 const int64_t blocks = rows < kMaxGenericBlocks ? rows : kMaxGenericBlocks;

@@ -2,7 +2,7 @@
 //
 // Fast path (head_dim 128, heads % 4 == 0, 16-byte aligned): a head of 128
 // bf16 is 256 bytes = 16 lanes x one 128-bit vector, so a wave holds four
-// heads of one token.  Lane l of a head holds elements 8(l%16) .. +7; the
+// heads of one token at a time, eight (two per lane) when heads % 8 == 0.  Lane l of a head holds elements 8(l%16) .. +7; the
 // RoPE partner of element p (p < 64) is p + 64, which sits in lane l ^ 8 of
 // the same 16-lane row and is fetched with one DPP row_ror:8 per dword (no
 // LDS).  Token and position are wave-uniform (scalar math).  The fused
@@ -31,6 +31,9 @@ namespace q3k
         constexpr int kHeadsPerWave = kWave / 16;
         constexpr int kWavesPerBlock = kBlock / kWave;
         constexpr uint32_t kNanPair = 0x7fc07fc0u;
+        // NT mode bits (loads | stores) and heads per lane, chosen by measurement.
+        constexpr int kNtmRope = 0;
+        constexpr int kNtmNormRope = 2;
 
         struct RopeShape
         {
@@ -53,90 +56,115 @@ namespace q3k
             return (pos >= 0 && pos < rs.table_positions) ? pos : -1;
         }
 
-        // Rotate the eight values held by this lane.  own: this lane's values;
-        // partner: the values of lane ^ 8.  First-half lanes compute
-        // x1*c - x2*s, second-half lanes x2*c + x1*s.
-        __device__ __forceinline__ Vec8 rotate8(const Vec8 &own, const Vec8 &partner, const float *cs, bool first_half)
-        {
-            const uint32_t sign = first_half ? 0x80000000u : 0u;
-            Vec8 r;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                const float c0 = cs[4 * k + 0], s0 = __uint_as_float(__float_as_uint(cs[4 * k + 1]) ^ sign);
-                const float c1 = cs[4 * k + 2], s1 = __uint_as_float(__float_as_uint(cs[4 * k + 3]) ^ sign);
-                const float a0 = bf_lo(own.d[k]) * c0;
-                const float b0 = bf_lo(partner.d[k]) * s0;
-                const float a1 = bf_hi(own.d[k]) * c1;
-                const float b1 = bf_hi(partner.d[k]) * s1;
-                r.d[k] = pack_rne(a0 + b0, a1 + b1);
-            }
-            return r;
-        }
-
-        __device__ __forceinline__ Vec8 partner_of(const Vec8 &v)
-        {
-            Vec8 p;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                p.d[k] = dpp_u<kDppRowRor8>(v.d[k]);
-            return p;
-        }
-
-        // One wave = four consecutive heads of one token.  Waves [0, q_waves)
-        // cover q (heads_q per token), the rest k (heads_k per token).
-        template <bool NORM>
+        // One wave = 4 * HG consecutive heads of one token (heads % (4 * HG)
+        // == 0): lane l of the wave works on heads head0 + l/16 + 4i, i < HG,
+        // elements 8(l%16) .. +7 of each.  The table row, the sign pattern and
+        // the norm weights depend only on the lane and the position, so they
+        // are loaded and unpacked once per wave.  Waves [0, q_waves) cover q
+        // (heads_q per token), the rest k (heads_k per token).
+        template <bool NORM, int NTM, int HG>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
             int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
             RopeShape rs, float eps)
         {
+            constexpr int kHeadsPerWaveHG = kHeadsPerWave * HG;
+            constexpr int kVecPerHead = kHeadDim / 8;
             const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
                                  __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             if (wave >= total_waves)
                 return;
             const int lane16 = threadIdx.x % 16;
-            const bool first_half = lane16 < 8;
-
             const bool is_q = wave < q_waves;
-            const int64_t head0 = (is_q ? wave : wave - q_waves) * kHeadsPerWave;
+            const int64_t head0 = (is_q ? wave : wave - q_waves) * kHeadsPerWaveHG;
             const int32_t heads = is_q ? heads_q : heads_k;
-            uint16_t *base = is_q ? q : k;
             const int64_t token = head0 / heads;
             const int64_t pos = token_position(rs, token);
 
-            Vec8 *hv = reinterpret_cast<Vec8 *>(base) + (head0 + (threadIdx.x % kWave) / 16) * (kHeadDim / 8) + lane16;
-            Vec8 x = *hv;
-            Vec8 wv;
-            if constexpr (NORM)
-                wv = reinterpret_cast<const Vec8 *>(is_q ? qw : kw)[lane16];
+            Vec8 *hv = reinterpret_cast<Vec8 *>(is_q ? q : k) +
+                       (head0 + (threadIdx.x % kWave) / 16) * kVecPerHead + lane16;
+            Vec8 x[HG];
+#pragma unroll
+            for (int i = 0; i < HG; ++i)
+                x[i] = load8<nt_load(NTM)>(hv + i * kHeadsPerWave * kVecPerHead);
 
             if (pos < 0)
             {
                 const Vec8 nan = {{kNanPair, kNanPair, kNanPair, kNanPair}};
-                *hv = nan;
+#pragma unroll
+                for (int i = 0; i < HG; ++i)
+                    store8<nt_store(NTM)>(hv + i * kHeadsPerWave * kVecPerHead, nan);
                 return;
             }
 
+            float wf[8];
+            if constexpr (NORM)
+            {
+                const Vec8 wv = reinterpret_cast<const Vec8 *>(is_q ? qw : kw)[lane16];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    wf[2 * j] = bf_lo(wv.d[j]);
+                    wf[2 * j + 1] = bf_hi(wv.d[j]);
+                }
+            }
+            // cos and sin of pairs 8(l%8) .. +7; first-half lanes use -sin so
+            // that both halves compute own * cos + partner * sin'.
             const F4 *crow = reinterpret_cast<const F4 *>(rs.cache + (pos * kHalf + (lane16 % 8) * 8) * 2);
-            float cs[16];
+            const uint32_t sign = lane16 < 8 ? 0x80000000u : 0u;
+            float cs[8], sn[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
                 const F4 t = crow[i];
-                cs[4 * i + 0] = t.v[0];
-                cs[4 * i + 1] = t.v[1];
-                cs[4 * i + 2] = t.v[2];
-                cs[4 * i + 3] = t.v[3];
+                cs[2 * i] = t.v[0];
+                sn[2 * i] = __uint_as_float(__float_as_uint(t.v[1]) ^ sign);
+                cs[2 * i + 1] = t.v[2];
+                sn[2 * i + 1] = __uint_as_float(__float_as_uint(t.v[3]) ^ sign);
             }
 
-            if constexpr (NORM)
+#pragma unroll
+            for (int i = 0; i < HG; ++i)
             {
-                const float total = group_sum<16>(sum_sq8(x));
-                x = norm_scale8(x, wv, inverse_rms(total, static_cast<float>(kHeadDim), eps));
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    v[2 * j] = bf_lo(x[i].d[j]);
+                    v[2 * j + 1] = bf_hi(x[i].d[j]);
+                }
+                if constexpr (NORM)
+                {
+                    // rms_norm over the head (128 values in 16 lanes), two roundings
+                    float ss[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        ss[j] = v[2 * j] * v[2 * j] + v[2 * j + 1] * v[2 * j + 1];
+                    const float total = group_sum<16>((ss[0] + ss[1]) + (ss[2] + ss[3]));
+                    const float inv = inverse_rms(total, 1.0f / static_cast<float>(kHeadDim), eps);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        const uint32_t n = pack_rne(v[2 * j] * inv, v[2 * j + 1] * inv);
+                        const uint32_t y = pack_rne(bf_lo(n) * wf[2 * j], bf_hi(n) * wf[2 * j + 1]);
+                        v[2 * j] = bf_lo(y);
+                        v[2 * j + 1] = bf_hi(y);
+                    }
+                }
+                // partner value (lane ^ 8) through DPP, folded into the multiply
+                Vec8 r;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    const float a0 = v[2 * j] * cs[2 * j];
+                    const float b0 = dpp_f<kDppRowRor8>(v[2 * j]) * sn[2 * j];
+                    const float a1 = v[2 * j + 1] * cs[2 * j + 1];
+                    const float b1 = dpp_f<kDppRowRor8>(v[2 * j + 1]) * sn[2 * j + 1];
+                    r.d[j] = pack_rne(a0 + b0, a1 + b1);
+                }
+                store8<nt_store(NTM)>(hv + i * kHeadsPerWave * kVecPerHead, r);
             }
-            *hv = rotate8(x, partner_of(x), cs, first_half);
         }
 
         // Generic RoPE: one thread per (token, head, pair), any even head_dim.
@@ -219,7 +247,28 @@ namespace q3k
             return Q3K_OK;
         }
 
-        int64_t waves_for(int64_t tokens, int32_t heads) { return tokens * heads / kHeadsPerWave; }
+        int64_t waves_for(int64_t tokens, int32_t heads, int hg) { return tokens * heads / (kHeadsPerWave * hg); }
+
+        template <bool NORM>
+        void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
+                          int64_t tokens, const RopeShape &rs, float eps, bool two_per_lane, hipStream_t stream)
+        {
+            constexpr int NTM = NORM ? kNtmNormRope : kNtmRope;
+            const int hg = two_per_lane ? 2 : 1;
+            const int64_t q_waves = waves_for(tokens, hq, hg);
+            const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, hg));
+            const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
+            if (two_per_lane)
+                rope_heads_kernel<NORM, NTM, 2><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+                    q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
+            else
+                rope_heads_kernel<NORM, NTM, 1><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+                    q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
+        }
+
+        // Launches stay far below 2^31 blocks for any tensor that fits in memory
+        // (4 heads of 256 bytes per wave).
+        bool grid_ok(int64_t tokens, int32_t heads) { return tokens * heads / 16 < (int64_t{1} << 31); }
     } // namespace
 } // namespace q3k
 
@@ -235,17 +284,10 @@ extern "C" int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, i
         return Q3K_OK;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    const int64_t waves = waves_for(tokens, heads);
-    const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (fast_ok(x, cache, heads, D) && blocks < (int64_t{1} << 31))
-    {
-        rope_heads_kernel<false><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
-            x, x, nullptr, nullptr, heads, heads, waves, waves, rs, 0.0f);
-    }
+    if (fast_ok(x, cache, heads, D) && grid_ok(tokens, heads))
+        launch_heads<false>(x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, heads % 8 == 0, s);
     else
-    {
         launch_generic_rope(x, heads, D, rs, s);
-    }
     return check_launch("apply_rope");
 }
 
@@ -270,13 +312,10 @@ extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *q
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "Q/K norm weights must be 2-byte aligned");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    const int64_t q_waves = waves_for(tokens, Hq);
-    const int64_t total = q_waves + waves_for(tokens, Hkv);
-    const int64_t blocks = (total + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) && blocks < (int64_t{1} << 31))
+    if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) &&
+        grid_ok(tokens, Hq + Hkv))
     {
-        rope_heads_kernel<true><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
-            q, k, qw, kw, Hq, Hkv, q_waves, total, rs, eps);
+        launch_heads<true>(q, k, qw, kw, Hq, Hkv, tokens, rs, eps, Hq % 8 == 0 && Hkv % 8 == 0, s);
         return check_launch("qk_norm_rope");
     }
     // Unfused fallback: per-head RMSNorm in place, then RoPE.

@@ -102,7 +102,7 @@ def test_rms_norm_kat(q3k, hip, oracle, shape):
     check_band(oracle, f"rms_norm kat {shape}", y, prim, lo, hi)
 
 
-RMS_CASES = [(16, 1024, 0), (1, 8, 0), (3, 16, 0), (5, 24, 0), (7, 64, 0), (100, 128, 0), (9, 200, 0), (4, 256, 0),
+RMS_CASES = [(16, 1024, 0), (5, 2048, 0), (3, 16384, 0), (2, 16392, 0), (4, 7168, 0), (6, 768, 0), (1, 8, 0), (3, 16, 0), (5, 24, 0), (7, 64, 0), (100, 128, 0), (9, 200, 0), (4, 256, 0),
              (6, 512, 0), (3, 1000, 0), (64, 4096, 0), (17, 5120, 0), (2, 8192, 0), (3, 8200, 0), (5, 257, 0),
              (7, 1024, 2), (33, 128, 2), (1, 1, 0)]
 
@@ -131,7 +131,8 @@ def test_rms_norm_config1(q3k, hip, oracle, synth, configs):
 
 
 @pytest.mark.parametrize("rows,n,offset", [(16, 1024, 0), (64, 4096, 0), (9, 5120, 0), (3, 8200, 0), (5, 257, 0),
-                                           (11, 1024, 2), (40, 128, 0)])
+                                           (11, 1024, 2), (40, 128, 0), (3, 2048, 0), (2, 16384, 0), (4, 768, 0),
+                                           (3, 7168, 0), (5, 512, 0)])
 def test_add_rms_norm(q3k, hip, oracle, synth, rows, n, offset):
     name = f"add_rms_norm rows={rows} N={n} offset={offset}"
     announce(name)
