@@ -16,8 +16,8 @@ sets (6 x 1.31 GB; the smallest per-op cycle, 6 x 80 MB of Q/K, is still far
 above the 256 MB Infinity Cache), so each launch reads its inputs from HBM.  ``value`` is the chain's algorithmic bytes (each
 compulsory byte once) divided by the measured time per step, inputs already
 resident in HBM.  Per-kernel durations come from back-to-back launches of
-each kernel alone (rotating over the same input sets) between one pair of
-HIP events.
+each kernel alone between one pair of HIP events, rotating over copies of
+its buffers whose cycle exceeds 1.5 GiB (so none is served from the cache).
 
 Also reported (not part of ``value``): the embedding gather and the final
 RMSNorm at config 4, the same chain built from the unfused drop-in ops in
@@ -143,14 +143,46 @@ def time_chain(hip, stream, sets, make_ops, steps, warmup):
     return start.elapsed_ms(stop) / steps
 
 
-def time_each_op(hip, stream, sets, make_ops, reps, warmup=2):
-    """Per-op duration: `reps` back-to-back launches of one op (rotating over
-    the input sets, so every launch reads from HBM) between one pair of
-    events; returns {op: ms per launch}."""
-    per_set = [make_ops(s) for s in sets]
+# Buffers each chain op touches (for its own rotation when timed alone).
+OP_BUFFERS = {
+    "add_rms_norm_attn": ("h1", "d1", "y1"),
+    "qk_norm_rope": ("q", "k"),
+    "add_rms_norm_mlp": ("h2", "d2", "y2"),
+    "silu_mul": ("g", "u", "o"),
+}
+UNFUSED_BUFFERS = {
+    "add_inplace": ("h1", "d1"), "rms_norm": ("h1", "y1"), "rms_norm_q": ("q",), "rms_norm_k": ("k",),
+    "rope_q": ("o",), "rope_k": ("y2",), "add_inplace_2": ("h2", "d2"), "rms_norm_2": ("h2", "y2"),
+    "silu_mul": ("g", "u", "o"),
+}
+MIN_CYCLE_BYTES = 3 << 29  # 1.5 GiB: 6x the 256 MB Infinity Cache
+
+
+def op_rotation(hip, sets, keys):
+    """Input sets for timing one op alone: enough copies of the op's own
+    buffers that one cycle over them exceeds MIN_CYCLE_BYTES (so no launch
+    finds its inputs in the Infinity Cache); other buffers are shared."""
+    per_set = sum(sets[0][k].nbytes for k in keys)
+    need = max(len(sets), -(-MIN_CYCLE_BYTES // per_set))
+    out = list(sets)
+    while len(out) < need:
+        extra = dict(sets[0])
+        for k in keys:
+            extra[k] = hip.DeviceBuffer(sets[0][k].nbytes)
+            extra[k].copy_from(sets[len(out) % len(sets)][k])
+        out.append(extra)
+    return out
+
+
+def time_each_op(hip, stream, sets, make_ops, reps, warmup=2, buffers=None):
+    """Per-op duration: `reps` back-to-back launches of one op, rotating over
+    input sets whose cycle exceeds the Infinity Cache (so every launch reads
+    from HBM), between one pair of events; returns {op: ms per launch}."""
     out = {}
-    for k, (name, _) in enumerate(per_set[0]):
-        out[name] = time_chain(hip, stream, sets, lambda s, k=k: [make_ops(s)[k]], reps, warmup)
+    for k, (name, _) in enumerate(make_ops(sets[0])):
+        rot = op_rotation(hip, sets, buffers[name]) if buffers and name in buffers else sets
+        out[name] = time_chain(hip, stream, rot, lambda s, k=k: [make_ops(s)[k]], max(reps, len(rot)), warmup)
+        del rot
     return out
 
 
@@ -250,7 +282,7 @@ def main():
           file=sys.stderr, flush=True)
     make_chain = lambda b: chain_ops(q3k, c, b, stream)  # noqa: E731
     ms_step = time_chain(hip, stream, sets, make_chain, args.steps, args.warmup)
-    per_op = time_each_op(hip, stream, sets, make_chain, args.steps)
+    per_op = time_each_op(hip, stream, sets, make_chain, args.steps, buffers=OP_BUFFERS)
 
     T, H, I = c.tokens, c.hidden, c.inter
     U = c.distinct_positions()
@@ -280,7 +312,7 @@ def main():
         print("[bench] timing unfused chain", file=sys.stderr, flush=True)
         make_unfused = lambda b: unfused_ops(q3k, c, b, stream)  # noqa: E731
         ms_unfused = time_chain(hip, stream, sets, make_unfused, max(5, args.steps // 2), 3)
-        per_unfused = time_each_op(hip, stream, sets, make_unfused, max(5, args.steps // 2))
+        per_unfused = time_each_op(hip, stream, sets, make_unfused, max(5, args.steps // 2), buffers=UNFUSED_BUFFERS)
         extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5),
                                    "per_op_ms": {k: round(v, 5) for k, v in per_unfused.items()},
                                    "fused_speedup": round(ms_unfused / ms_step, 3)}

@@ -20,7 +20,7 @@ namespace q3k
         constexpr int kUnrollSilu = 2;
         constexpr int kNtmSilu = 3;
         constexpr int kUnrollAdd = 1;
-        constexpr int kNtmAdd = 1;
+        constexpr int kNtmAdd = 3;
         constexpr int kNtmCopy = 3;
 
         // exp(x) for the SiLU denominator: Cody-Waite style split of

@@ -14,7 +14,7 @@ namespace q3k
     {
         constexpr int kTokensPerBlock = kBlock / kWave;
         constexpr int kVpt = 8;
-        constexpr int kNtm = 0;  // measured: plain loads/stores are faster for the random-row gather
+        constexpr int kNtm = 2;  // measured: plain loads (random rows), non-temporal stores
 
         template <int NTM>
         __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(

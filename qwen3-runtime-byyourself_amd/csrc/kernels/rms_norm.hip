@@ -9,7 +9,7 @@
 // over 128) give each row an aligned group of lanes and reduce the sum of
 // squares with DPP inside the wave; rows up to 1024 elements use one wave;
 // wider rows (hidden 2048 .. 16384) use one block of up to eight waves per
-// row whose wave sums meet in LDS behind one barrier.  Stores are
+// row whose wave sums meet in LDS behind one barrier.  Loads and stores are
 // non-temporal.  The mapping per width was chosen by measurement on MI355X.
 //
 // Generic path (any N, any alignment): one 256-thread block per row, scalar
@@ -204,9 +204,13 @@ namespace q3k
             }
         }
 
-        // Non-temporal stores, plain loads: the fastest mode measured on MI355X
-        // for every row width of the model (1024 .. 8192), fused or not.
-        constexpr int kNtmRows = 2;
+        // Non-temporal mode bits (loads | stores), measured on MI355X with
+        // input cycles far above the Infinity Cache: non-temporal loads and
+        // stores for every row width, except narrow rows without the fused
+        // add, where plain loads are faster.
+        constexpr int kNtmBlock = 3;
+        template <bool ADD>
+        constexpr int ntm_rows() { return ADD ? 3 : 2; }
 
         template <int G, int VPT, bool ADD>
         void launch_rows(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
@@ -214,7 +218,7 @@ namespace q3k
         {
             constexpr int kRowsPerBlock = kBlock / G;
             const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-            rms_rows_kernel<G, VPT, ADD, kNtmRows><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
+            rms_rows_kernel<G, VPT, ADD, ntm_rows<ADD>()><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
                 h, d, w, y, rows, nvec, inv_n, eps);
         }
 
@@ -222,7 +226,7 @@ namespace q3k
         void launch_block(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
                           int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
         {
-            rms_block_kernel<WPR, VPT, ADD, kNtmRows><<<dim3(static_cast<unsigned>(rows)), dim3(WPR * kWave), 0, stream>>>(
+            rms_block_kernel<WPR, VPT, ADD, kNtmBlock><<<dim3(static_cast<unsigned>(rows)), dim3(WPR * kWave), 0, stream>>>(
                 h, d, w, y, rows, nvec, inv_n, eps);
         }
 

@@ -2,7 +2,8 @@
 //
 // Fast path (head_dim 128, heads % 4 == 0, 16-byte aligned): a head of 128
 // bf16 is 256 bytes = 16 lanes x one 128-bit vector, so a wave holds four
-// heads of one token at a time, eight (two per lane) when heads % 8 == 0.  Lane l of a head holds elements 8(l%16) .. +7; the
+// heads of one token at a time; a lane processes up to four heads (16 per
+// wave) when the head count allows.  Lane l of a head holds elements 8(l%16) .. +7; the
 // RoPE partner of element p (p < 64) is p + 64, which sits in lane l ^ 8 of
 // the same 16-lane row and is fetched with one DPP row_ror:8 per dword (no
 // LDS).  Token and position are wave-uniform (scalar math).  The fused
@@ -32,8 +33,8 @@ namespace q3k
         constexpr int kWavesPerBlock = kBlock / kWave;
         constexpr uint32_t kNanPair = 0x7fc07fc0u;
         // NT mode bits (loads | stores) and heads per lane, chosen by measurement.
-        constexpr int kNtmRope = 0;
-        constexpr int kNtmNormRope = 2;
+        constexpr int kNtmRope = 3;
+        constexpr int kNtmNormRope = 3;
 
         struct RopeShape
         {
@@ -60,30 +61,19 @@ namespace q3k
         // == 0): lane l of the wave works on heads head0 + l/16 + 4i, i < HG,
         // elements 8(l%16) .. +7 of each.  The table row, the sign pattern and
         // the norm weights depend only on the lane and the position, so they
-        // are loaded and unpacked once per wave.  Waves [0, q_waves) cover q
-        // (heads_q per token), the rest k (heads_k per token).
+        // are loaded and unpacked once per wave.  head0 and the token are
+        // wave-uniform and below 2^31 (checked by the launcher).
         template <bool NORM, int NTM, int HG>
-        __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
-            uint16_t *__restrict__ q, uint16_t *__restrict__ k,
-            const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
-            int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
-            RopeShape rs, float eps)
+        __device__ __forceinline__ void rope_heads(uint16_t *base, const uint16_t *w, uint32_t head0, uint32_t heads,
+                                                   const RopeShape &rs, float eps)
         {
-            constexpr int kHeadsPerWaveHG = kHeadsPerWave * HG;
             constexpr int kVecPerHead = kHeadDim / 8;
-            const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
-                                 __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-            if (wave >= total_waves)
-                return;
             const int lane16 = threadIdx.x % 16;
-            const bool is_q = wave < q_waves;
-            const int64_t head0 = (is_q ? wave : wave - q_waves) * kHeadsPerWaveHG;
-            const int32_t heads = is_q ? heads_q : heads_k;
-            const int64_t token = head0 / heads;
+            const uint32_t token = head0 / heads;
             const int64_t pos = token_position(rs, token);
 
-            Vec8 *hv = reinterpret_cast<Vec8 *>(is_q ? q : k) +
-                       (head0 + (threadIdx.x % kWave) / 16) * kVecPerHead + lane16;
+            Vec8 *hv = reinterpret_cast<Vec8 *>(base) +
+                       (static_cast<int64_t>(head0) + (threadIdx.x % kWave) / 16) * kVecPerHead + lane16;
             Vec8 x[HG];
 #pragma unroll
             for (int i = 0; i < HG; ++i)
@@ -101,7 +91,7 @@ namespace q3k
             float wf[8];
             if constexpr (NORM)
             {
-                const Vec8 wv = reinterpret_cast<const Vec8 *>(is_q ? qw : kw)[lane16];
+                const Vec8 wv = reinterpret_cast<const Vec8 *>(w)[lane16];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                 {
@@ -165,6 +155,26 @@ namespace q3k
                 }
                 store8<nt_store(NTM)>(hv + i * kHeadsPerWave * kVecPerHead, r);
             }
+        }
+
+        // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with HGK.
+        template <bool NORM, int NTM, int HGQ, int HGK>
+        __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
+            uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+            const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
+            int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
+            RopeShape rs, float eps)
+        {
+            const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+                                 __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+            if (wave >= total_waves)
+                return;
+            if (wave < q_waves)
+                rope_heads<NORM, NTM, HGQ>(q, qw, static_cast<uint32_t>(wave * kHeadsPerWave * HGQ),
+                                           static_cast<uint32_t>(heads_q), rs, eps);
+            else
+                rope_heads<NORM, NTM, HGK>(k, kw, static_cast<uint32_t>((wave - q_waves) * kHeadsPerWave * HGK),
+                                           static_cast<uint32_t>(heads_k), rs, eps);
         }
 
         // Generic RoPE: one thread per (token, head, pair), any even head_dim.
@@ -249,26 +259,45 @@ namespace q3k
 
         int64_t waves_for(int64_t tokens, int32_t heads, int hg) { return tokens * heads / (kHeadsPerWave * hg); }
 
-        template <bool NORM>
-        void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
-                          int64_t tokens, const RopeShape &rs, float eps, bool two_per_lane, hipStream_t stream)
+        // Heads per lane: 4 when the head count allows it (32 or 64 query
+        // heads), else 2 (8 KV heads), else 1.
+        int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
+
+        template <bool NORM, int HGQ, int HGK>
+        void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
+                             int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream)
         {
             constexpr int NTM = NORM ? kNtmNormRope : kNtmRope;
-            const int hg = two_per_lane ? 2 : 1;
-            const int64_t q_waves = waves_for(tokens, hq, hg);
-            const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, hg));
+            const int64_t q_waves = waves_for(tokens, hq, HGQ);
+            const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            if (two_per_lane)
-                rope_heads_kernel<NORM, NTM, 2><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
-                    q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
-            else
-                rope_heads_kernel<NORM, NTM, 1><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
-                    q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
+            rope_heads_kernel<NORM, NTM, HGQ, HGK><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+                q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
         }
 
-        // Launches stay far below 2^31 blocks for any tensor that fits in memory
-        // (4 heads of 256 bytes per wave).
-        bool grid_ok(int64_t tokens, int32_t heads) { return tokens * heads / 16 < (int64_t{1} << 31); }
+        template <bool NORM>
+        void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
+                          int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream)
+        {
+            const int gq = heads_per_lane(hq);
+            const int gk = k == nullptr ? gq : heads_per_lane(hk);
+            const int key = gq * 10 + gk;
+            switch (key)
+            {
+            case 44: launch_heads_hg<NORM, 4, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 42: launch_heads_hg<NORM, 4, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 41: launch_heads_hg<NORM, 4, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 24: launch_heads_hg<NORM, 2, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 22: launch_heads_hg<NORM, 2, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 21: launch_heads_hg<NORM, 2, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 14: launch_heads_hg<NORM, 1, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 12: launch_heads_hg<NORM, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            default: launch_heads_hg<NORM, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            }
+        }
+
+        // The fast kernel indexes heads with 32-bit wave-uniform arithmetic.
+        bool grid_ok(int64_t tokens, int32_t heads) { return tokens * heads < (int64_t{1} << 31); }
     } // namespace
 } // namespace q3k
 
@@ -285,7 +314,7 @@ extern "C" int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, i
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
     if (fast_ok(x, cache, heads, D) && grid_ok(tokens, heads))
-        launch_heads<false>(x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, heads % 8 == 0, s);
+        launch_heads<false>(x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, s);
     else
         launch_generic_rope(x, heads, D, rs, s);
     return check_launch("apply_rope");
@@ -315,7 +344,7 @@ extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *q
     if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) &&
         grid_ok(tokens, Hq + Hkv))
     {
-        launch_heads<true>(q, k, qw, kw, Hq, Hkv, tokens, rs, eps, Hq % 8 == 0 && Hkv % 8 == 0, s);
+        launch_heads<true>(q, k, qw, kw, Hq, Hkv, tokens, rs, eps, s);
         return check_launch("qk_norm_rope");
     }
     // Unfused fallback: per-head RMSNorm in place, then RoPE.
