@@ -19,6 +19,7 @@ namespace q3k
         // vectors per thread (per operand) and non-temporal mode bits.
         constexpr int kUnrollSilu = 2;
         constexpr int kNtmSilu = 3;
+        constexpr int kPrioSilu = 1;  // wave priority while loads are issued
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
         constexpr int kNtmCopy = 3;
@@ -128,7 +129,7 @@ namespace q3k
 
         // OP 0: out = silu(a) * b.  OP 1: out = a + b (out == a for add_inplace).
         // Each thread handles U vectors spaced one block apart.
-        template <int OP, int U, int NTM>
+        template <int OP, int U, int NTM, int PR>
         __global__ __launch_bounds__(kBlock) void binary_vec_kernel(
             const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t nvec, int64_t n)
         {
@@ -138,6 +139,8 @@ namespace q3k
             const int64_t base = static_cast<int64_t>(blockIdx.x) * (kBlock * U) + threadIdx.x;
 
             Vec8 x[U], y[U];
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(PR);
 #pragma unroll
             for (int i = 0; i < U; ++i)
             {
@@ -148,6 +151,8 @@ namespace q3k
                     y[i] = load8<nt_load(NTM)>(bv + j);
                 }
             }
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int i = 0; i < U; ++i)
             {
@@ -178,12 +183,13 @@ namespace q3k
         {
             constexpr int U = OP == 0 ? kUnrollSilu : kUnrollAdd;
             constexpr int NTM = OP == 0 ? kNtmSilu : kNtmAdd;
+            constexpr int PR = OP == 0 ? kPrioSilu : 0;
             constexpr int64_t kVecPerBlock = static_cast<int64_t>(kBlock) * U;
             const int64_t nvec = n / 8;
             const int64_t blocks = (nvec + kVecPerBlock - 1) / kVecPerBlock;
             if (aligned16(a) && aligned16(b) && aligned16(out) && blocks < (int64_t{1} << 31))
             {
-                binary_vec_kernel<OP, U, NTM><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
+                binary_vec_kernel<OP, U, NTM, PR><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
                     a, b, out, nvec, n);
             }
             else

@@ -96,62 +96,104 @@ namespace q3k
                     store8<nt_store(NTM)>(yrow + lane + i * G, norm_scale8(x[i], wv[i], inv));
         }
 
-        // WPR waves per row (one row per block), VPT vectors per lane; the
-        // wave sums meet in LDS behind one barrier.
-        template <int WPR, int VPT, bool ADD, int NTM>
+        // WPR waves per row, R consecutive rows per block, VPT vectors per
+        // lane and row; the wave sums of all R rows meet in LDS behind one
+        // barrier.  PR > 0 raises the wave priority while the loads are issued.
+        template <int WPR, int VPT, int R, bool ADD, int NTM, int PR>
         __global__ __launch_bounds__(WPR * kWave) void rms_block_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
             int64_t rows, int nvec, float inv_n, float eps)
         {
             constexpr int kThreads = WPR * kWave;
-            __shared__ float wave_sums[WPR];
+            __shared__ float wave_sums[R][WPR];
             const int t = threadIdx.x;
-            const int64_t row = blockIdx.x;
-            const int64_t row_offset = row * static_cast<int64_t>(nvec);
-            Vec8 *hrow = reinterpret_cast<Vec8 *>(h) + row_offset;
+            const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
             const Vec8 *wvec = reinterpret_cast<const Vec8 *>(w);
-            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row_offset;
 
-            Vec8 x[VPT], dv[VPT], wv[VPT];
+            Vec8 x[R][VPT], dv[R][VPT], wv[VPT];
             bool live[VPT];
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(PR);
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
             {
                 const int j = t + i * kThreads;
                 live[i] = j < nvec;
                 if (live[i])
-                {
-                    x[i] = load8<nt_load(NTM)>(hrow + j);
-                    if constexpr (ADD)
-                        dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
                     wv[i] = wvec[j];
-                }
             }
-            const float partial = add_and_square<VPT, ADD>(x, dv, live);
-            if constexpr (ADD)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
             {
+                const int64_t row = row0 + r;
+                if (row >= rows)
+                    break;
+                const int64_t row_offset = row * static_cast<int64_t>(nvec);
 #pragma unroll
                 for (int i = 0; i < VPT; ++i)
+                {
+                    const int j = t + i * kThreads;
                     if (live[i])
-                        store8<nt_store(NTM)>(hrow + t + i * kThreads, x[i]);
+                    {
+                        x[r][i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(h) + row_offset + j);
+                        if constexpr (ADD)
+                            dv[r][i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
+                    }
+                }
             }
-            float total = group_sum<kWave>(partial);
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(0);
+
+            float total[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+            {
+                total[r] = 0.0f;
+                const int64_t row = row0 + r;
+                if (row >= rows)
+                    break;
+                const float partial = add_and_square<VPT, ADD>(x[r], dv[r], live);
+                if constexpr (ADD)
+                {
+#pragma unroll
+                    for (int i = 0; i < VPT; ++i)
+                        if (live[i])
+                            store8<nt_store(NTM)>(reinterpret_cast<Vec8 *>(h) + row * nvec + t + i * kThreads, x[r][i]);
+                }
+                total[r] = group_sum<kWave>(partial);
+            }
             if constexpr (WPR > 1)
             {
                 if (t % kWave == 0)
-                    wave_sums[t / kWave] = total;
+                {
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        wave_sums[r][t / kWave] = total[r];
+                }
                 __syncthreads();
-                total = 0.0f;
 #pragma unroll
-                for (int k = 0; k < WPR; ++k)
-                    total += wave_sums[k];
+                for (int r = 0; r < R; ++r)
+                {
+                    total[r] = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < WPR; ++k)
+                        total[r] += wave_sums[r][k];
+                }
             }
-            const float inv = inverse_rms(total, inv_n, eps);
 #pragma unroll
-            for (int i = 0; i < VPT; ++i)
-                if (live[i])
-                    store8<nt_store(NTM)>(yrow + t + i * kThreads, norm_scale8(x[i], wv[i], inv));
+            for (int r = 0; r < R; ++r)
+            {
+                const int64_t row = row0 + r;
+                if (row >= rows)
+                    break;
+                const float inv = inverse_rms(total[r], inv_n, eps);
+                Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * static_cast<int64_t>(nvec);
+#pragma unroll
+                for (int i = 0; i < VPT; ++i)
+                    if (live[i])
+                        store8<nt_store(NTM)>(yrow + t + i * kThreads, norm_scale8(x[r][i], wv[i], inv));
+            }
         }
 
         // Block-wide sum for the generic kernel: wave sums through LDS, then
@@ -222,12 +264,20 @@ namespace q3k
                 h, d, w, y, rows, nvec, inv_n, eps);
         }
 
+        // Rows per block and load priority of the block kernel (measured).
+        constexpr int kRowsPerBlockAdd = 1;
+        constexpr int kRowsPerBlockNorm = 1;
+        constexpr int kPrioAdd = 1;
+        constexpr int kPrioNorm = 0;
+
         template <int WPR, int VPT, bool ADD>
         void launch_block(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
                           int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
         {
-            rms_block_kernel<WPR, VPT, ADD, kNtmBlock><<<dim3(static_cast<unsigned>(rows)), dim3(WPR * kWave), 0, stream>>>(
-                h, d, w, y, rows, nvec, inv_n, eps);
+            constexpr int R = ADD ? kRowsPerBlockAdd : kRowsPerBlockNorm;
+            const int64_t blocks = (rows + R - 1) / R;
+            rms_block_kernel<WPR, VPT, R, ADD, kNtmBlock, ADD ? kPrioAdd : kPrioNorm>
+                <<<dim3(static_cast<unsigned>(blocks)), dim3(WPR * kWave), 0, stream>>>(h, d, w, y, rows, nvec, inv_n, eps);
         }
 
         template <int VPT, bool ADD>
