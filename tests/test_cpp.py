@@ -1,0 +1,32 @@
+"""The C++ tests of the qwen3:: layer (tests/cpp/), built by build(): CPU
+contract tests here, GPU op tests under the gpu marker."""
+import os
+import subprocess
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(REPO, "tests", "cpp", "build")
+CPU_TESTS = ["core_metadata_test", "tensor_view_test", "buffer_cpu_test", "tensor_cpu_test", "ops_validation_cpu_test"]
+GPU_TESTS = ["buffer_gpu_test", "ops_gpu_test", "fused_gpu_test"]
+
+
+def _run(name, env=None, timeout=120):
+    exe = os.path.join(BIN, name)
+    if not os.path.exists(exe):
+        pytest.fail(f"{exe} is not built; run __graft_entry__.build()")
+    proc = subprocess.run([exe], capture_output=True, text=True, timeout=timeout, env=env)
+    assert proc.returncode == 0, f"{name} failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}"
+    assert "passed" in proc.stdout
+
+
+@pytest.mark.parametrize("name", CPU_TESTS)
+def test_cpp_cpu(name):
+    _run(name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", GPU_TESTS)
+def test_cpp_gpu(name):
+    _run(name, timeout=300)
+

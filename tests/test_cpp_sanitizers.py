@@ -1,0 +1,32 @@
+"""The host-side C++ tests rebuilt with AddressSanitizer +
+UndefinedBehaviorSanitizer (g++, host code only; CPU only)."""
+import glob
+import os
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+def test_cpp_cpu_under_sanitizers():
+    """Core tensor layer + host tests rebuilt with -fsanitize=address,undefined."""
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    core = sorted(glob.glob(os.path.join(REPO, "qwen3-runtime-byyourself_amd", "csrc", "core", "*.cpp")))
+    inc = [f"-I{os.path.join(REPO, 'include')}", "-I/opt/rocm/include", f"-I{os.path.join(REPO, 'oracle')}",
+           f"-I{os.path.join(REPO, 'tests', 'cpp')}"]
+    flags = ["-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+             "-fno-sanitize-recover=undefined", "-D__HIP_PLATFORM_AMD__"]
+    libs = [os.path.join(REPO, "oracle", "build", "libq3k_oracle.so"), "-L/opt/rocm/lib", "-lamdhip64",
+            "-Wl,-rpath,/opt/rocm/lib", "-Wl,-rpath," + os.path.join(REPO, "oracle", "build"), "-pthread"]
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0", UBSAN_OPTIONS="print_stacktrace=1")
+    with tempfile.TemporaryDirectory() as tmp:
+        for name in ["core_metadata_test", "tensor_view_test", "buffer_cpu_test", "tensor_cpu_test"]:
+            exe = os.path.join(tmp, name)
+            src = os.path.join(REPO, "tests", "cpp", name + ".cpp")
+            build = subprocess.run(["g++", *flags, *inc, src, *core, "-o", exe, *libs], capture_output=True, text=True)
+            assert build.returncode == 0, build.stderr[-3000:]
+            proc = subprocess.run([exe], capture_output=True, text=True, timeout=120, env=env)
+            assert proc.returncode == 0, f"{name} under sanitizers:\n{proc.stdout}\n{proc.stderr[-3000:]}"
