@@ -1,0 +1,71 @@
+"""Writes the golden fixtures of tests/golden/ from the CPU oracle.
+
+Inputs are the reference tests' known-answer patterns (tests/kat.py, from the
+reference's tests/unit/*_cuda_test.cpp) and BASELINE config 1 (x [16, 1024] ~
+N(0,1), w ~ N(1, 0.1), eps 1e-6, seed 0).  The reference itself cannot run
+here (CUDA, and its src/core is missing), so these vectors record the
+oracle's outputs after it was pinned by tests/test_oracle_pins.py; they guard
+the oracle (and, through the GPU tests, the kernels) against drift.
+
+Run from the repository root: python tests/golden/make_golden.py
+"""
+import importlib
+import importlib.util
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, REPO)
+sys.path.insert(0, os.path.dirname(HERE))
+
+
+def load_oracle():
+    spec = importlib.util.spec_from_file_location("q3k_oracle", os.path.join(REPO, "oracle", "q3k_oracle.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def fixtures(oracle):
+    import kat
+
+    synth = importlib.import_module("qwen3-runtime-byyourself_amd.synth")
+    configs = importlib.import_module("qwen3-runtime-byyourself_amd.configs")
+    out = {}
+    for shape in [(2, 3, 1024), (2, 3, 4, 128)]:
+        x, w = kat.rms_input(shape), kat.rms_weight(shape[-1])
+        y, lo, hi = oracle.rms_norm(x, w, 1e-6, nthreads=1)
+        out["kat_rms_norm_" + "x".join(map(str, shape))] = dict(x=x, w=w, y=y, lo=lo, hi=hi)
+    B, S, Hq, Hkv, D, P, start = kat.ROPE_B, kat.ROPE_S, kat.ROPE_HQ, kat.ROPE_HKV, kat.ROPE_D, kat.ROPE_P, kat.ROPE_START
+    cache = oracle.build_rope_cache(P, D, kat.ROPE_THETA)
+    q = kat.rope_values(B * S * Hq * D, 0).reshape(B, S, Hq * D)
+    k = kat.rope_values(B * S * Hkv * D, 5).reshape(B, S, Hkv * D)
+    qo, qlo, qhi = oracle.rope(q, B, S, Hq, D, cache, start, nthreads=1)
+    ko, klo, khi = oracle.rope(k, B, S, Hkv, D, cache, start, nthreads=1)
+    out["kat_rope"] = dict(q=q, k=k, cache=cache, q_out=qo, q_lo=qlo, q_hi=qhi, k_out=ko, k_lo=klo, k_hi=khi)
+    r, d, g, u = kat.elementwise_inputs()
+    so, slo, shi = oracle.silu_mul(g, u, nthreads=1)
+    out["kat_elementwise"] = dict(residual=r, delta=d, gate=g, up=u, add_out=oracle.add_inplace(r, d, nthreads=1),
+                                  silu_out=so, silu_lo=slo, silu_hi=shi)
+    table, ids = kat.embedding_inputs()
+    out["kat_embedding"] = dict(table=table, ids=ids, out=oracle.embedding(ids, table, nthreads=1))
+    c = configs.CONFIGS["c1"]
+    x = synth.normal_bf16(c.seed, configs.TID_X, (c.seq, c.hidden))
+    w = synth.normal_bf16(c.seed, configs.TID_WF, (c.hidden,), mean=1.0, std=0.1)
+    y, lo, hi = oracle.rms_norm(x, w, 1e-6, nthreads=1)
+    out["config1_rms_norm"] = dict(x=x, w=w, y=y, lo=lo, hi=hi)
+    return out
+
+
+def main():
+    oracle = load_oracle()
+    for name, arrays in fixtures(oracle).items():
+        np.savez_compressed(os.path.join(HERE, name + ".npz"), **arrays)
+        print("wrote", name)
+
+
+if __name__ == "__main__":
+    main()
