@@ -3,7 +3,7 @@
 one MI355X (gfx950), through the C ABI of libq3k.so.
 
 A step is one pass of the per-layer non-GEMM chain over one batch of
-synthetic input at BASELINE config 4 (Qwen3-8B prefill, T = 8192 tokens as
+synthetic input at benchmark config 4 (Qwen3-8B prefill, T = 8192 tokens as
 4 sequences x 2048, positions 0..2047 per sequence):
 
   add_rms_norm  h1 += d1; y1 = rmsnorm(h1)     [8192, 4096]   attention residual + post-attention norm
@@ -352,7 +352,7 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded normals, BASELINE config shapes)",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded normals at the benchmark config shapes)",
         "config": {"workload": f"{c.name}: per-layer non-GEMM chain (add_rms_norm x2, qk_norm_rope, silu_mul)",
                    "tokens": T, "hidden": H, "intermediate": I, "heads_q": c.heads_q, "heads_kv": c.heads_kv,
                    "head_dim": D, "chain_bytes": chain_bytes, "input_sets": len(sets)},

@@ -1,7 +1,7 @@
 """Writes the golden fixtures of tests/golden/ from the CPU oracle.
 
 Inputs are the reference tests' known-answer patterns (tests/kat.py, from the
-reference's tests/unit/*_cuda_test.cpp) and BASELINE config 1 (x [16, 1024] ~
+reference's tests/unit/*_cuda_test.cpp) and benchmark config 1 (x [16, 1024] ~
 N(0,1), w ~ N(1, 0.1), eps 1e-6, seed 0).  The reference itself cannot run
 here (CUDA, and its src/core is missing), so these vectors record the
 oracle's outputs after it was pinned by tests/test_oracle_pins.py; they guard

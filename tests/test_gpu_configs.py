@@ -1,4 +1,4 @@
-"""Every op of every benchmark config at its full size (BASELINE configs
+"""Every op of every benchmark config at its full size (benchmark configs
 2-5), through the C ABI, against the oracle on the host.
 
 Inputs follow the configs' stated distributions (synth.py; unstated ones:

@@ -119,7 +119,7 @@ def test_rms_norm_shapes(q3k, hip, oracle, synth, rows, n, offset):
 
 
 def test_rms_norm_config1(q3k, hip, oracle, synth, configs):
-    """x [16, 1024] ~ N(0,1), w ~ N(1, 0.1), eps 1e-6, seed 0."""
+    """Benchmark config 1: x [16, 1024] ~ N(0,1), w ~ N(1, 0.1), eps 1e-6, seed 0."""
     announce("rms_norm c1")
     c = configs.CONFIGS["c1"]
     x = synth.normal_bf16(c.seed, configs.TID_X, (c.seq, c.hidden))
