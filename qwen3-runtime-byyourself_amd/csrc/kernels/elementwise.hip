@@ -20,6 +20,9 @@ namespace q3k
         constexpr int kUnrollSilu = 2;
         constexpr int kNtmSilu = 3;
         constexpr int kPrioSilu = 1;  // wave priority while loads are issued
+        // XCD-contiguous tile remapping measured slower for both streams.
+        constexpr bool kRemapSilu = false;
+        constexpr bool kRemapAdd = false;
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
         constexpr int kNtmCopy = 3;
@@ -129,14 +132,15 @@ namespace q3k
 
         // OP 0: out = silu(a) * b.  OP 1: out = a + b (out == a for add_inplace).
         // Each thread handles U vectors spaced one block apart.
-        template <int OP, int U, int NTM, int PR>
+        template <int OP, int U, int NTM, int PR, bool REMAP>
         __global__ __launch_bounds__(kBlock) void binary_vec_kernel(
             const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t nvec, int64_t n)
         {
             const Vec8 *av = reinterpret_cast<const Vec8 *>(a);
             const Vec8 *bv = reinterpret_cast<const Vec8 *>(b);
             Vec8 *ov = reinterpret_cast<Vec8 *>(out);
-            const int64_t base = static_cast<int64_t>(blockIdx.x) * (kBlock * U) + threadIdx.x;
+            const int64_t tile = tile_index<REMAP>(blockIdx.x, gridDim.x);
+            const int64_t base = tile * (kBlock * U) + threadIdx.x;
 
             Vec8 x[U], y[U];
             if constexpr (PR > 0)
@@ -161,7 +165,7 @@ namespace q3k
                     store8<nt_store(NTM)>(ov + j, apply8<OP>(x[i], y[i]));
             }
 
-            if (blockIdx.x == 0)
+            if (tile == 0)
             {
                 for (int64_t e = nvec * 8 + threadIdx.x; e < n; e += kBlock)
                     out[e] = apply1<OP>(a[e], b[e]);
@@ -184,12 +188,13 @@ namespace q3k
             constexpr int U = OP == 0 ? kUnrollSilu : kUnrollAdd;
             constexpr int NTM = OP == 0 ? kNtmSilu : kNtmAdd;
             constexpr int PR = OP == 0 ? kPrioSilu : 0;
+            constexpr bool REMAP = OP == 0 ? kRemapSilu : kRemapAdd;
             constexpr int64_t kVecPerBlock = static_cast<int64_t>(kBlock) * U;
             const int64_t nvec = n / 8;
             const int64_t blocks = (nvec + kVecPerBlock - 1) / kVecPerBlock;
             if (aligned16(a) && aligned16(b) && aligned16(out) && blocks < (int64_t{1} << 31))
             {
-                binary_vec_kernel<OP, U, NTM, PR><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
+                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
                     a, b, out, nvec, n);
             }
             else

@@ -151,6 +151,21 @@ namespace q3k
         return __builtin_amdgcn_rsqf(sum * inv_n + eps);
     }
 
+    // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
+    // XCD b % 8).  With REMAP the block works on tile (b % 8) * (n / 8) + b / 8
+    // instead, so each XCD streams one contiguous eighth of the tiles; tiles
+    // past the last multiple of 8 keep their own index.
+    template <bool REMAP>
+    __device__ __forceinline__ uint32_t tile_index(uint32_t block, uint32_t blocks)
+    {
+        if constexpr (!REMAP)
+            return block;
+        const uint32_t per = blocks / 8;
+        if (block >= per * 8)
+            return block;
+        return (block % 8) * per + block / 8;
+    }
+
     // NT mode bits of a kernel: bit 0 = non-temporal loads, bit 1 = non-temporal stores.
     constexpr bool nt_load(int ntm) { return (ntm & 1) != 0; }
     constexpr bool nt_store(int ntm) { return (ntm & 2) != 0; }

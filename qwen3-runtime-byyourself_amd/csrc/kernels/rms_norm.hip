@@ -99,7 +99,7 @@ namespace q3k
         // WPR waves per row, R consecutive rows per block, VPT vectors per
         // lane and row; the wave sums of all R rows meet in LDS behind one
         // barrier.  PR > 0 raises the wave priority while the loads are issued.
-        template <int WPR, int VPT, int R, bool ADD, int NTM, int PR>
+        template <int WPR, int VPT, int R, bool ADD, int NTM, int PR, bool REMAP>
         __global__ __launch_bounds__(WPR * kWave) void rms_block_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
@@ -108,7 +108,7 @@ namespace q3k
             constexpr int kThreads = WPR * kWave;
             __shared__ float wave_sums[R][WPR];
             const int t = threadIdx.x;
-            const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+            const int64_t row0 = static_cast<int64_t>(tile_index<REMAP>(blockIdx.x, gridDim.x)) * R;
             const Vec8 *wvec = reinterpret_cast<const Vec8 *>(w);
 
             Vec8 x[R][VPT], dv[R][VPT], wv[VPT];
@@ -269,6 +269,7 @@ namespace q3k
         constexpr int kRowsPerBlockNorm = 1;
         constexpr int kPrioAdd = 1;
         constexpr int kPrioNorm = 0;
+        constexpr bool kRemapRows = false;  // XCD-contiguous rows measured slower
 
         template <int WPR, int VPT, bool ADD>
         void launch_block(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
@@ -276,7 +277,7 @@ namespace q3k
         {
             constexpr int R = ADD ? kRowsPerBlockAdd : kRowsPerBlockNorm;
             const int64_t blocks = (rows + R - 1) / R;
-            rms_block_kernel<WPR, VPT, R, ADD, kNtmBlock, ADD ? kPrioAdd : kPrioNorm>
+            rms_block_kernel<WPR, VPT, R, ADD, kNtmBlock, ADD ? kPrioAdd : kPrioNorm, kRemapRows>
                 <<<dim3(static_cast<unsigned>(blocks)), dim3(WPR * kWave), 0, stream>>>(h, d, w, y, rows, nvec, inv_n, eps);
         }
 

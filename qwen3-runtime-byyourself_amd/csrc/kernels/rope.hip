@@ -35,6 +35,7 @@ namespace q3k
         // NT mode bits (loads | stores) and heads per lane, chosen by measurement.
         constexpr int kNtmRope = 3;
         constexpr int kNtmNormRope = 3;
+        constexpr bool kRemapHeads = false;  // XCD-contiguous tiles measured slower
 
         struct RopeShape
         {
@@ -163,14 +164,14 @@ namespace q3k
         }
 
         // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with HGK.
-        template <bool NORM, int NTM, int HGQ, int HGK>
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
             int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
             RopeShape rs, float eps)
         {
-            const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+            const int64_t wave = static_cast<int64_t>(tile_index<REMAP>(blockIdx.x, gridDim.x)) * kWavesPerBlock +
                                  __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             if (wave >= total_waves)
                 return;
@@ -276,7 +277,7 @@ namespace q3k
             const int64_t q_waves = waves_for(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            rope_heads_kernel<NORM, NTM, HGQ, HGK><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
                 q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
         }
 
