@@ -337,12 +337,47 @@ def main():
                     b.free()
             table = hip.DeviceBuffer.from_array(
                 synth.normal_bf16(c.seed, configs.TID_TABLE, (configs.VOCAB, H)))
-            ids = hip.DeviceBuffer.from_array(synth.token_ids(c.seed, configs.TID_IDS, (T,), configs.VOCAB))
-            out = hip.DeviceBuffer(T * H * 2)
-            ms_e = time_chain(hip, stream, [0], lambda _: [
-                ("embedding", lambda: q3k.embedding(ids, T, table, configs.VOCAB, H, out, stream))], 20, 3)
+            w = sets[0]["w1"]
+            # Each set gathers its own T random rows and writes its own outputs; one cycle over the sets
+            # moves >= MIN_CYCLE_BYTES, so neither the gathered rows nor the outputs stay in the Infinity Cache.
+            per_set = 3 * T * H * 2
+            emb_sets = [{"ids": hip.DeviceBuffer.from_array(
+                             synth.token_ids(c.seed + k, configs.TID_IDS, (T,), configs.VOCAB)),
+                         "out": hip.DeviceBuffer(T * H * 2), "y": hip.DeviceBuffer(T * H * 2)}
+                        for k in range(-(-MIN_CYCLE_BYTES // per_set))]
+            ms_e = time_chain(hip, stream, emb_sets, lambda e: [
+                ("embedding", lambda: q3k.embedding(e["ids"], T, table, configs.VOCAB, H, e["out"], stream))],
+                max(20, len(emb_sets)), 3)
             eb = configs.bytes_embedding(T, H)
             extras["embedding"] = {"ms": round(ms_e, 5), "bytes": eb, "GB/s": round(eb / (ms_e * 1e-3) / 1e9, 1)}
+            # embedding + first input norm fused (model.cpp:118 -> decoder_layer.cpp:72) against the pair
+            ms_en = time_chain(hip, stream, emb_sets, lambda e: [
+                ("embedding_rms_norm", lambda: q3k.embedding_rms_norm(e["ids"], T, table, configs.VOCAB, H, w, EPS,
+                                                                      e["out"], e["y"], stream))],
+                max(20, len(emb_sets)), 3)
+            ms_pair = time_chain(hip, stream, emb_sets, lambda e: [
+                ("embedding", lambda: q3k.embedding(e["ids"], T, table, configs.VOCAB, H, e["out"], stream)),
+                ("rms_norm", lambda: q3k.rms_norm(e["out"], w, e["y"], T, H, EPS, stream))],
+                max(20, len(emb_sets)), 3)
+            enb = configs.bytes_embedding_rms_norm(T, H)
+            extras["embedding_rms_norm"] = {"ms": round(ms_en, 5), "bytes": enb,
+                                            "GB/s": round(enb / (ms_en * 1e-3) / 1e9, 1),
+                                            "unfused_ms": round(ms_pair, 5),
+                                            "fused_speedup": round(ms_pair / ms_en, 3)}
+            # final norm of each sequence's last token only (model.cpp:146 + lm_head.cpp:123-181): B rows,
+            # a latency-bound launch, reported against the full-sequence final norm it replaces
+            Bq, Sq = c.batch, c.seq
+            yl = hip.DeviceBuffer(Bq * H * 2)
+            e0 = emb_sets[0]
+            ms_last = time_chain(hip, stream, [0], lambda _: [
+                ("add_rms_norm_last_token", lambda: q3k.add_rms_norm_rows(e0["out"], e0["y"], w, yl, Bq, Sq - 1, Sq, H,
+                                                                          EPS, stream))], 50, 5)
+            extras["add_rms_norm_last_token"] = {"ms": round(ms_last, 5), "rows": Bq,
+                                                 "full_final_norm_ms": extras["rms_norm_final"]["ms"]}
+            yl.free()
+            for e in emb_sets:
+                for buf in e.values():
+                    buf.free()
 
     cpu = None
     if not args.no_cpu_baseline:

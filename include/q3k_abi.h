@@ -87,6 +87,44 @@ Q3K_API int q3k_add_rms_norm_bf16(uint16_t *h, const uint16_t *d, const uint16_t
                           q3k_stream_t stream);
 
 /*
+ * RMSNorm of selected rows into a compact output: y row i = rms_norm(x row
+ * first_row + i * row_stride), i in [0, count).  With first_row = S - 1 and
+ * row_stride = S over x [B, S, N] this is the final norm of the last token of
+ * every sequence, the only rows the LM head reads.
+ * Replaces rms_norm at src/model/model.cpp:146 followed by the last-token
+ * select of src/model/lm_head.cpp:123-181.
+ */
+Q3K_API int q3k_rms_norm_rows_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y,
+                           int64_t count, int64_t first_row, int64_t row_stride,
+                           int64_t N, float eps, q3k_stream_t stream);
+
+/*
+ * Fused residual add + RMSNorm of selected rows: for i in [0, count), with
+ * r = first_row + i * row_stride: h row r = RNE(h row r + d row r) (in place)
+ * and y row i = rms_norm(h row r).  Other rows of h are left untouched (after
+ * the last layer only the last tokens' residuals are still needed).
+ * Replaces add_inplace at src/model/decoder_layer.cpp:94 of the last layer,
+ * rms_norm at src/model/model.cpp:146 and the last-token select of
+ * src/model/lm_head.cpp:123-181.
+ */
+Q3K_API int q3k_add_rms_norm_rows_bf16(uint16_t *h, const uint16_t *d, const uint16_t *w,
+                               uint16_t *y, int64_t count, int64_t first_row,
+                               int64_t row_stride, int64_t N, float eps,
+                               q3k_stream_t stream);
+
+/*
+ * Fused embedding gather + RMSNorm: hidden[t, :] = table[ids[t], :] (a zero
+ * row for ids outside [0, V)), then y = rms_norm(hidden, w).  The table row is
+ * read once; hidden (the residual stream) and y are written.
+ * Replaces embedding_lookup at src/model/model.cpp:118 followed by the first
+ * layer's input rms_norm at src/model/decoder_layer.cpp:72.
+ */
+Q3K_API int q3k_embedding_rms_norm_bf16(const int32_t *ids, int64_t T,
+                                const uint16_t *table, int64_t V, int64_t H,
+                                const uint16_t *w, float eps,
+                                uint16_t *hidden, uint16_t *y, q3k_stream_t stream);
+
+/*
  * In-place residual add: d[i] = RNE(d[i] + s[i]), n elements.
  * Replaces qwen3::ops::add_inplace, src/ops/elementwise.cu:133-157 (kernel :21-36).
  */

@@ -73,6 +73,9 @@ SIGNATURES = {
     "q3k_embedding_bf16": [_p, _i64, _p, _i64, _i64, _p, _p],
     "q3k_rms_norm_bf16": [_p, _p, _p, _i64, _i64, _f32, _p],
     "q3k_add_rms_norm_bf16": [_p, _p, _p, _p, _i64, _i64, _f32, _p],
+    "q3k_rms_norm_rows_bf16": [_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p],
+    "q3k_add_rms_norm_rows_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p],
+    "q3k_embedding_rms_norm_bf16": [_p, _i64, _p, _i64, _i64, _p, _f32, _p, _p, _p],
     "q3k_add_inplace_bf16": [_p, _p, _i64, _p],
     "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
@@ -144,6 +147,20 @@ def rms_norm(x, w, y, rows, N, eps, stream=None):
 
 def add_rms_norm(h, d, w, y, rows, N, eps, stream=None):
     _check(load().q3k_add_rms_norm_bf16(_ptr(h), _ptr(d), _ptr(w), _ptr(y), rows, N, eps, _ptr(stream)))
+
+
+def rms_norm_rows(x, w, y, count, first_row, row_stride, N, eps, stream=None):
+    _check(load().q3k_rms_norm_rows_bf16(_ptr(x), _ptr(w), _ptr(y), count, first_row, row_stride, N, eps, _ptr(stream)))
+
+
+def add_rms_norm_rows(h, d, w, y, count, first_row, row_stride, N, eps, stream=None):
+    _check(load().q3k_add_rms_norm_rows_bf16(_ptr(h), _ptr(d), _ptr(w), _ptr(y), count, first_row, row_stride, N, eps,
+                                             _ptr(stream)))
+
+
+def embedding_rms_norm(ids, T, table, V, H, w, eps, hidden, y, stream=None):
+    _check(load().q3k_embedding_rms_norm_bf16(_ptr(ids), T, _ptr(table), V, H, _ptr(w), eps, _ptr(hidden), _ptr(y),
+                                              _ptr(stream)))
 
 
 def add_inplace(d, s, n, stream=None):

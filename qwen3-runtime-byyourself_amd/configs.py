@@ -56,6 +56,11 @@ def bytes_rms_norm(T, H):
     return 2 * T * H * 2 + 2 * H
 
 
+def bytes_embedding_rms_norm(T, H):
+    """ids + gathered rows in, hidden and normalized rows out, plus the weight."""
+    return 4 * T + 3 * T * H * 2 + 2 * H
+
+
 def bytes_add_inplace(T, H):
     return 3 * T * H * 2
 

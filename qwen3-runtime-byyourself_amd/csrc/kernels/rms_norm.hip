@@ -25,9 +25,61 @@ namespace q3k
 {
     namespace
     {
-        // Normalise the row slice held by this thread: h = RNE(h + d) (ADD),
-        // then the partial sum of squares of the rounded values.
-        template <int VPT, bool ADD>
+        // What a launch normalises.  kNorm: y = rms_norm(x); kAddNorm:
+        // h = RNE(h + d) written back, y = rms_norm(h); kGatherNorm: the row
+        // is table[ids[i]] (zero when the id is outside [0, vocab)), written
+        // to h as the residual stream, and y = rms_norm(row).
+        enum RowMode
+        {
+            kNorm = 0,
+            kAddNorm = 1,
+            kGatherNorm = 2,
+        };
+
+        // Output row i (of y, and of h in gather mode) reads input row
+        // first + i * stride of h and d; plain launches use first 0, stride 1.
+        struct RowMap
+        {
+            int64_t first;
+            int64_t stride;
+            const int32_t *ids;
+            const uint16_t *table;
+            int64_t vocab;
+        };
+
+        // Source of output row `out_row`: its input vectors, or nullptr for a
+        // gathered row whose id is out of range (the row is zero).
+        template <int MODE>
+        __device__ __forceinline__ const Vec8 *row_source(const uint16_t *h, const RowMap &map, int64_t out_row,
+                                                          int nvec)
+        {
+            if constexpr (MODE == kGatherNorm)
+            {
+                const int32_t id = map.ids[out_row];
+                if (id < 0 || static_cast<int64_t>(id) >= map.vocab)
+                    return nullptr;
+                return reinterpret_cast<const Vec8 *>(map.table) + static_cast<int64_t>(id) * nvec;
+            }
+            else
+            {
+                return reinterpret_cast<const Vec8 *>(h) + (map.first + out_row * map.stride) * nvec;
+            }
+        }
+
+        // Where the updated residual of output row `out_row` goes (kAddNorm,
+        // kGatherNorm).
+        template <int MODE>
+        __device__ __forceinline__ Vec8 *residual_row(uint16_t *h, const RowMap &map, int64_t out_row, int nvec)
+        {
+            if constexpr (MODE == kGatherNorm)
+                return reinterpret_cast<Vec8 *>(h) + out_row * nvec;
+            else
+                return reinterpret_cast<Vec8 *>(h) + (map.first + out_row * map.stride) * nvec;
+        }
+
+        // h = RNE(h + d) for the add mode, then the partial sum of squares of
+        // the (rounded) values held by this thread.
+        template <int VPT, int MODE>
         __device__ __forceinline__ float add_and_square(Vec8 (&x)[VPT], const Vec8 (&dv)[VPT], const bool (&live)[VPT])
         {
             float partial = 0.0f;
@@ -36,7 +88,7 @@ namespace q3k
             {
                 if (!live[i])
                     continue;
-                if constexpr (ADD)
+                if constexpr (MODE == kAddNorm)
                 {
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
@@ -47,12 +99,37 @@ namespace q3k
             return partial;
         }
 
+        // Loads of one row slice: x (and d) from their rows, the weights.
+        template <int VPT, int MODE, int NTM>
+        __device__ __forceinline__ void load_row(const Vec8 *src, const uint16_t *d, const RowMap &map, int64_t out_row,
+                                                 int nvec, const Vec8 *wvec, int first_vec, int vec_step, Vec8 (&x)[VPT],
+                                                 Vec8 (&dv)[VPT], Vec8 (&wv)[VPT], bool (&live)[VPT])
+        {
+            const Vec8 zero = {{0u, 0u, 0u, 0u}};
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+            {
+                const int j = first_vec + i * vec_step;
+                live[i] = j < nvec;
+                if (!live[i])
+                    continue;
+                if constexpr (MODE == kGatherNorm)
+                    x[i] = src != nullptr ? load8<false>(src + j) : zero;
+                else
+                    x[i] = load8<nt_load(NTM)>(src + j);
+                if constexpr (MODE == kAddNorm)
+                    dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) +
+                                                (map.first + out_row * map.stride) * nvec + j);
+                wv[i] = wvec[j];
+            }
+        }
+
         // Group of G lanes per row (G <= 64), VPT vectors per lane.
-        template <int G, int VPT, bool ADD, int NTM>
+        template <int G, int VPT, int MODE, int NTM>
         __global__ __launch_bounds__(kBlock) void rms_rows_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
-            int64_t rows, int nvec, float inv_n, float eps)
+            int64_t rows, int nvec, float inv_n, float eps, RowMap map)
         {
             constexpr int kRowsPerBlock = kBlock / G;
             const int lane = threadIdx.x % G;
@@ -60,140 +137,76 @@ namespace q3k
             if (row >= rows)
                 return;
 
-            const int64_t row_offset = row * static_cast<int64_t>(nvec);
-            Vec8 *hrow = reinterpret_cast<Vec8 *>(h) + row_offset;
-            const Vec8 *wvec = reinterpret_cast<const Vec8 *>(w);
-            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row_offset;
-
-            // Issue every load of the row (and the weights) before any use.
             Vec8 x[VPT], dv[VPT], wv[VPT];
             bool live[VPT];
-#pragma unroll
-            for (int i = 0; i < VPT; ++i)
+            load_row<VPT, MODE, NTM>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
+                                     reinterpret_cast<const Vec8 *>(w), lane, G, x, dv, wv, live);
+            const float partial = add_and_square<VPT, MODE>(x, dv, live);
+            if constexpr (MODE != kNorm)
             {
-                const int j = lane + i * G;
-                live[i] = j < nvec;
-                if (live[i])
-                {
-                    x[i] = load8<nt_load(NTM)>(hrow + j);
-                    if constexpr (ADD)
-                        dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
-                    wv[i] = wvec[j];
-                }
-            }
-            const float partial = add_and_square<VPT, ADD>(x, dv, live);
-            if constexpr (ADD)
-            {
+                Vec8 *hrow = residual_row<MODE>(h, map, row, nvec);
 #pragma unroll
                 for (int i = 0; i < VPT; ++i)
                     if (live[i])
                         store8<nt_store(NTM)>(hrow + lane + i * G, x[i]);
             }
             const float inv = inverse_rms(group_sum<G>(partial), inv_n, eps);
+            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * nvec;
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
                 if (live[i])
                     store8<nt_store(NTM)>(yrow + lane + i * G, norm_scale8(x[i], wv[i], inv));
         }
 
-        // WPR waves per row, R consecutive rows per block, VPT vectors per
-        // lane and row; the wave sums of all R rows meet in LDS behind one
-        // barrier.  PR > 0 raises the wave priority while the loads are issued.
-        template <int WPR, int VPT, int R, bool ADD, int NTM, int PR, bool REMAP>
+        // One row per block of WPR waves, VPT vectors per lane; the wave sums
+        // meet in LDS behind one barrier.  PR > 0 raises the wave priority
+        // while the loads are issued.
+        template <int WPR, int VPT, int MODE, int NTM, int PR, bool REMAP>
         __global__ __launch_bounds__(WPR * kWave) void rms_block_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
-            int64_t rows, int nvec, float inv_n, float eps)
+            int64_t rows, int nvec, float inv_n, float eps, RowMap map)
         {
             constexpr int kThreads = WPR * kWave;
-            __shared__ float wave_sums[R][WPR];
+            __shared__ float wave_sums[WPR];
             const int t = threadIdx.x;
-            const int64_t row0 = static_cast<int64_t>(tile_index<REMAP>(blockIdx.x, gridDim.x)) * R;
-            const Vec8 *wvec = reinterpret_cast<const Vec8 *>(w);
+            const int64_t row = tile_index<REMAP>(blockIdx.x, gridDim.x);
 
-            Vec8 x[R][VPT], dv[R][VPT], wv[VPT];
+            Vec8 x[VPT], dv[VPT], wv[VPT];
             bool live[VPT];
             if constexpr (PR > 0)
                 __builtin_amdgcn_s_setprio(PR);
-#pragma unroll
-            for (int i = 0; i < VPT; ++i)
-            {
-                const int j = t + i * kThreads;
-                live[i] = j < nvec;
-                if (live[i])
-                    wv[i] = wvec[j];
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-            {
-                const int64_t row = row0 + r;
-                if (row >= rows)
-                    break;
-                const int64_t row_offset = row * static_cast<int64_t>(nvec);
-#pragma unroll
-                for (int i = 0; i < VPT; ++i)
-                {
-                    const int j = t + i * kThreads;
-                    if (live[i])
-                    {
-                        x[r][i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(h) + row_offset + j);
-                        if constexpr (ADD)
-                            dv[r][i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) + row_offset + j);
-                    }
-                }
-            }
+            load_row<VPT, MODE, NTM>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
+                                     reinterpret_cast<const Vec8 *>(w), t, kThreads, x, dv, wv, live);
             if constexpr (PR > 0)
                 __builtin_amdgcn_s_setprio(0);
 
-            float total[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
+            const float partial = add_and_square<VPT, MODE>(x, dv, live);
+            if constexpr (MODE != kNorm)
             {
-                total[r] = 0.0f;
-                const int64_t row = row0 + r;
-                if (row >= rows)
-                    break;
-                const float partial = add_and_square<VPT, ADD>(x[r], dv[r], live);
-                if constexpr (ADD)
-                {
-#pragma unroll
-                    for (int i = 0; i < VPT; ++i)
-                        if (live[i])
-                            store8<nt_store(NTM)>(reinterpret_cast<Vec8 *>(h) + row * nvec + t + i * kThreads, x[r][i]);
-                }
-                total[r] = group_sum<kWave>(partial);
-            }
-            if constexpr (WPR > 1)
-            {
-                if (t % kWave == 0)
-                {
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        wave_sums[r][t / kWave] = total[r];
-                }
-                __syncthreads();
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                {
-                    total[r] = 0.0f;
-#pragma unroll
-                    for (int k = 0; k < WPR; ++k)
-                        total[r] += wave_sums[r][k];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-            {
-                const int64_t row = row0 + r;
-                if (row >= rows)
-                    break;
-                const float inv = inverse_rms(total[r], inv_n, eps);
-                Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * static_cast<int64_t>(nvec);
+                Vec8 *hrow = residual_row<MODE>(h, map, row, nvec);
 #pragma unroll
                 for (int i = 0; i < VPT; ++i)
                     if (live[i])
-                        store8<nt_store(NTM)>(yrow + t + i * kThreads, norm_scale8(x[r][i], wv[i], inv));
+                        store8<nt_store(NTM)>(hrow + t + i * kThreads, x[i]);
             }
+            float total = group_sum<kWave>(partial);
+            if constexpr (WPR > 1)
+            {
+                if (t % kWave == 0)
+                    wave_sums[t / kWave] = total;
+                __syncthreads();
+                total = 0.0f;
+#pragma unroll
+                for (int k = 0; k < WPR; ++k)
+                    total += wave_sums[k];
+            }
+            const float inv = inverse_rms(total, inv_n, eps);
+            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * nvec;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (live[i])
+                    store8<nt_store(NTM)>(yrow + t + i * kThreads, norm_scale8(x[i], wv[i], inv));
         }
 
         // Block-wide sum for the generic kernel: wave sums through LDS, then
@@ -213,34 +226,56 @@ namespace q3k
             return total;
         }
 
-        template <bool ADD>
+        // Any width, any alignment: one 256-thread block per row, scalar
+        // accesses, two passes over the row.
+        template <int MODE>
         __global__ __launch_bounds__(kBlock) void rms_rows_generic_kernel(
             uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-            int64_t rows, int64_t n, float eps)
+            int64_t rows, int64_t n, float eps, RowMap map)
         {
             __shared__ float scratch[kBlock / kWave];
             const float inv_n = 1.0f / static_cast<float>(n);
             for (int64_t row = blockIdx.x; row < rows; row += gridDim.x)
             {
-                uint16_t *hr = h + row * n;
-                const uint16_t *dr = d + row * n;
+                const uint16_t *src;
+                uint16_t *hr;
+                bool zero = false;
+                if constexpr (MODE == kGatherNorm)
+                {
+                    const int32_t id = map.ids[row];
+                    zero = id < 0 || static_cast<int64_t>(id) >= map.vocab;
+                    src = map.table + (zero ? 0 : static_cast<int64_t>(id) * n);
+                    hr = h + row * n;
+                }
+                else
+                {
+                    hr = h + (map.first + row * map.stride) * n;
+                    src = hr;
+                }
+                const uint16_t *dr = d + (map.first + row * map.stride) * n;
                 uint16_t *yr = y + row * n;
                 float partial = 0.0f;
                 for (int64_t c = threadIdx.x; c < n; c += blockDim.x)
                 {
-                    float v = bf_to_f(hr[c]);
-                    if constexpr (ADD)
+                    float v = zero ? 0.0f : bf_to_f(src[c]);
+                    if constexpr (MODE == kAddNorm)
                     {
                         const uint16_t s = f_to_bf(v + bf_to_f(dr[c]));
                         hr[c] = s;
                         v = bf_to_f(s);
+                    }
+                    else if constexpr (MODE == kGatherNorm)
+                    {
+                        hr[c] = zero ? uint16_t{0} : src[c];
                     }
                     partial += v * v;
                 }
                 const float inv = inverse_rms(block_sum(partial, scratch), inv_n, eps);
                 for (int64_t c = threadIdx.x; c < n; c += blockDim.x)
                 {
-                    const float nrm = bf_to_f(f_to_bf(bf_to_f(hr[c]) * inv));
+                    // reads back the (rounded) residual this thread wrote in pass 1
+                    const float x = MODE == kNorm ? bf_to_f(src[c]) : bf_to_f(hr[c]);
+                    const float nrm = bf_to_f(f_to_bf(x * inv));
                     yr[c] = f_to_bf(nrm * bf_to_f(w[c]));
                 }
             }
@@ -249,52 +284,61 @@ namespace q3k
         // Non-temporal mode bits (loads | stores), measured on MI355X with
         // input cycles far above the Infinity Cache: non-temporal loads and
         // stores for every row width, except narrow rows without the fused
-        // add, where plain loads are faster.
-        constexpr int kNtmBlock = 3;
-        template <bool ADD>
-        constexpr int ntm_rows() { return ADD ? 3 : 2; }
-
-        template <int G, int VPT, bool ADD>
-        void launch_rows(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                         int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
-        {
-            constexpr int kRowsPerBlock = kBlock / G;
-            const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-            rms_rows_kernel<G, VPT, ADD, ntm_rows<ADD>()><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
-                h, d, w, y, rows, nvec, inv_n, eps);
-        }
-
-        // Rows per block and load priority of the block kernel (measured).
-        constexpr int kRowsPerBlockAdd = 1;
-        constexpr int kRowsPerBlockNorm = 1;
-        constexpr int kPrioAdd = 1;
-        constexpr int kPrioNorm = 0;
+        // add, where plain loads are faster.  Gathered rows use plain loads
+        // (random rows, as in the embedding kernel).
+        template <int MODE>
+        constexpr int ntm_block() { return MODE == kGatherNorm ? 2 : 3; }
+        template <int MODE>
+        constexpr int ntm_rows() { return MODE == kNorm ? 2 : MODE == kAddNorm ? 3 : 2; }
+        // Wave priority raised while loads are issued (measured: helps the fused add).
+        template <int MODE>
+        constexpr int prio_block() { return MODE == kAddNorm ? 1 : 0; }
         constexpr bool kRemapRows = false;  // XCD-contiguous rows measured slower
 
-        template <int WPR, int VPT, bool ADD>
-        void launch_block(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                          int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
+        struct Launch
         {
-            constexpr int R = ADD ? kRowsPerBlockAdd : kRowsPerBlockNorm;
-            const int64_t blocks = (rows + R - 1) / R;
-            rms_block_kernel<WPR, VPT, R, ADD, kNtmBlock, ADD ? kPrioAdd : kPrioNorm, kRemapRows>
-                <<<dim3(static_cast<unsigned>(blocks)), dim3(WPR * kWave), 0, stream>>>(h, d, w, y, rows, nvec, inv_n, eps);
+            uint16_t *h;
+            const uint16_t *d;
+            const uint16_t *w;
+            uint16_t *y;
+            int64_t rows;
+            int nvec;
+            float inv_n;
+            float eps;
+            RowMap map;
+            hipStream_t stream;
+        };
+
+        template <int G, int VPT, int MODE>
+        void launch_rows(const Launch &l)
+        {
+            constexpr int kRowsPerBlock = kBlock / G;
+            const int64_t blocks = (l.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+            rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>()><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, l.stream>>>(
+                l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
         }
 
-        template <int VPT, bool ADD>
-        bool launch_block_waves(int waves, uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                                int64_t rows, int nvec, float inv_n, float eps, hipStream_t stream)
+        template <int WPR, int VPT, int MODE>
+        void launch_block(const Launch &l)
+        {
+            rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows>
+                <<<dim3(static_cast<unsigned>(l.rows)), dim3(WPR * kWave), 0, l.stream>>>(
+                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+        }
+
+        template <int VPT, int MODE>
+        bool launch_block_waves(int waves, const Launch &l)
         {
             switch (waves)
             {
-            case 1: launch_block<1, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 2: launch_block<2, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 3: launch_block<3, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 4: launch_block<4, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 5: launch_block<5, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 6: launch_block<6, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 7: launch_block<7, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
-            case 8: launch_block<8, VPT, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream); return true;
+            case 1: launch_block<1, VPT, MODE>(l); return true;
+            case 2: launch_block<2, VPT, MODE>(l); return true;
+            case 3: launch_block<3, VPT, MODE>(l); return true;
+            case 4: launch_block<4, VPT, MODE>(l); return true;
+            case 5: launch_block<5, VPT, MODE>(l); return true;
+            case 6: launch_block<6, VPT, MODE>(l); return true;
+            case 7: launch_block<7, VPT, MODE>(l); return true;
+            case 8: launch_block<8, VPT, MODE>(l); return true;
             default: return false;
             }
         }
@@ -304,53 +348,53 @@ namespace q3k
         //                 (per-head norms, 128 elements = 16 lanes);
         //   nvec <= 128:  one wave per row, 1-2 vectors per lane (hidden 1024);
         //   nvec <= 2048: one row per block of up to 8 waves; one vector per lane
-        //                 for the fused add when nvec <= 512 (hidden <= 4096),
-        //                 else two (four beyond 8192 elements).
-        template <bool ADD>
-        bool launch_fast(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                         int64_t rows, int64_t n, float eps, hipStream_t stream)
+        //                 for the fused add and the gather when nvec <= 512
+        //                 (hidden <= 4096), else two (four beyond 8192 elements).
+        template <int MODE>
+        bool launch_fast(const Launch &l)
         {
-            const int nvec = static_cast<int>(n / 8);
-            const float inv_n = 1.0f / static_cast<float>(n);
+            const int nvec = l.nvec;
             if (nvec <= 1)
-                launch_rows<1, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<1, 1, MODE>(l);
             else if (nvec <= 2)
-                launch_rows<2, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<2, 1, MODE>(l);
             else if (nvec <= 4)
-                launch_rows<4, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<4, 1, MODE>(l);
             else if (nvec <= 8)
-                launch_rows<8, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<8, 1, MODE>(l);
             else if (nvec <= 16)
-                launch_rows<16, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<16, 1, MODE>(l);
             else if (nvec <= 32)
-                launch_rows<32, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<32, 1, MODE>(l);
             else if (nvec <= 64)
-                launch_rows<64, 1, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<64, 1, MODE>(l);
             else if (nvec <= 128)
-                launch_rows<64, 2, ADD>(h, d, w, y, rows, nvec, inv_n, eps, stream);
-            else if (ADD && nvec <= 512)
-                return launch_block_waves<1, ADD>((nvec + 63) / 64, h, d, w, y, rows, nvec, inv_n, eps, stream);
+                launch_rows<64, 2, MODE>(l);
+            else if (MODE != kNorm && nvec <= 512)
+                return launch_block_waves<1, MODE>((nvec + 63) / 64, l);
             else if (nvec <= 1024)
-                return launch_block_waves<2, ADD>((nvec + 127) / 128, h, d, w, y, rows, nvec, inv_n, eps, stream);
+                return launch_block_waves<2, MODE>((nvec + 127) / 128, l);
             else
-                return launch_block_waves<4, ADD>((nvec + 255) / 256, h, d, w, y, rows, nvec, inv_n, eps, stream);
+                return launch_block_waves<4, MODE>((nvec + 255) / 256, l);
             return true;
         }
 
         constexpr int64_t kMaxFastN = 8 * kWave * 4 * 8; // 16384 elements per row
         constexpr int64_t kMaxGenericBlocks = 1 << 20;
 
-        template <bool ADD>
-        int rms_dispatch(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
-                         int64_t rows, int64_t n, float eps, hipStream_t stream, const char *name)
+        template <int MODE>
+        int rms_dispatch(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y, int64_t rows, int64_t n,
+                         float eps, const RowMap &map, hipStream_t stream, const char *name)
         {
             const bool fast = (n % 8 == 0) && n <= kMaxFastN && aligned16(h) && aligned16(w) && aligned16(y) &&
-                              (!ADD || aligned16(d)) && rows < (int64_t{1} << 31);
-            if (!(fast && launch_fast<ADD>(h, d, w, y, rows, n, eps, stream)))
+                              (MODE != kAddNorm || aligned16(d)) && (MODE != kGatherNorm || aligned16(map.table)) &&
+                              rows < (int64_t{1} << 31);
+            const Launch l{h, d, w, y, rows, static_cast<int>(n / 8), 1.0f / static_cast<float>(n), eps, map, stream};
+            if (!(fast && launch_fast<MODE>(l)))
             {
                 const int64_t blocks = rows < kMaxGenericBlocks ? rows : kMaxGenericBlocks;
-                rms_rows_generic_kernel<ADD><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
-                    h, d, w, y, rows, n, eps);
+                rms_rows_generic_kernel<MODE><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
+                    h, d, w, y, rows, n, eps, map);
             }
             return check_launch(name);
         }
@@ -371,6 +415,24 @@ namespace q3k
                 return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm pointers must be 2-byte aligned");
             return Q3K_OK;
         }
+
+        // Rows first + i * stride, i < count, must lie in [0, INT64_MAX / n).
+        int validate_rows(int64_t count, int64_t first, int64_t stride, int64_t n)
+        {
+            if (first < 0 || stride < 0)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm row selection cannot be negative");
+            if (count > 0)
+            {
+                const int64_t limit = INT64_MAX / n;
+                if (stride > 0 && count - 1 > (limit - 1 - first) / stride)
+                    return set_error(Q3K_ERR_OVERFLOW, "RMSNorm row selection overflows");
+                if (first >= limit)
+                    return set_error(Q3K_ERR_OVERFLOW, "RMSNorm row selection overflows");
+            }
+            return Q3K_OK;
+        }
+
+        constexpr RowMap kPlainRows{0, 1, nullptr, nullptr, 0};
     } // namespace
 
     // In-place generic RMSNorm (y = x), used by the fused Q/K op's fallback.
@@ -379,8 +441,8 @@ namespace q3k
         if (rows == 0)
             return Q3K_OK;
         const int64_t blocks = rows < kMaxGenericBlocks ? rows : kMaxGenericBlocks;
-        rms_rows_generic_kernel<false><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
-            x, nullptr, w, x, rows, n, eps);
+        rms_rows_generic_kernel<kNorm><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(
+            x, nullptr, w, x, rows, n, eps, kPlainRows);
         return check_launch("rms_norm (generic)");
     }
 } // namespace q3k
@@ -393,8 +455,8 @@ extern "C" int q3k_rms_norm_bf16(const uint16_t *x, const uint16_t *w, uint16_t 
         return st;
     if (rows == 0)
         return Q3K_OK;
-    // The fast kernels read x through the h slot; x is never written when ADD is false.
-    return rms_dispatch<false>(const_cast<uint16_t *>(x), nullptr, w, y, rows, N, eps,
+    // x is read through the h slot and never written in this mode.
+    return rms_dispatch<kNorm>(const_cast<uint16_t *>(x), nullptr, w, y, rows, N, eps, kPlainRows,
                                reinterpret_cast<hipStream_t>(stream), "rms_norm");
 }
 
@@ -411,5 +473,64 @@ extern "C" int q3k_add_rms_norm_bf16(uint16_t *h, const uint16_t *d, const uint1
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm pointers must be 2-byte aligned");
     if (rows == 0)
         return Q3K_OK;
-    return rms_dispatch<true>(h, d, w, y, rows, N, eps, reinterpret_cast<hipStream_t>(stream), "add_rms_norm");
+    return rms_dispatch<kAddNorm>(h, d, w, y, rows, N, eps, kPlainRows, reinterpret_cast<hipStream_t>(stream),
+                                  "add_rms_norm");
+}
+
+extern "C" int q3k_rms_norm_rows_bf16(const uint16_t *x, const uint16_t *w, uint16_t *y, int64_t count,
+                                      int64_t first_row, int64_t row_stride, int64_t N, float eps,
+                                      q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_common(x, w, y, count, N, eps))
+        return st;
+    if (const int st = validate_rows(count, first_row, row_stride, N))
+        return st;
+    if (count == 0)
+        return Q3K_OK;
+    const RowMap map{first_row, row_stride, nullptr, nullptr, 0};
+    return rms_dispatch<kNorm>(const_cast<uint16_t *>(x), nullptr, w, y, count, N, eps, map,
+                               reinterpret_cast<hipStream_t>(stream), "rms_norm_rows");
+}
+
+extern "C" int q3k_add_rms_norm_rows_bf16(uint16_t *h, const uint16_t *d, const uint16_t *w, uint16_t *y,
+                                          int64_t count, int64_t first_row, int64_t row_stride, int64_t N,
+                                          float eps, q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_common(h, w, y, count, N, eps))
+        return st;
+    if (const int st = validate_rows(count, first_row, row_stride, N))
+        return st;
+    if (count > 0 && d == nullptr)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "add_rms_norm delta pointer is null");
+    if (!aligned_to(d, 2))
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm pointers must be 2-byte aligned");
+    if (count == 0)
+        return Q3K_OK;
+    const RowMap map{first_row, row_stride, nullptr, nullptr, 0};
+    return rms_dispatch<kAddNorm>(h, d, w, y, count, N, eps, map, reinterpret_cast<hipStream_t>(stream),
+                                  "add_rms_norm_rows");
+}
+
+extern "C" int q3k_embedding_rms_norm_bf16(const int32_t *ids, int64_t T, const uint16_t *table, int64_t V,
+                                           int64_t H, const uint16_t *w, float eps, uint16_t *hidden, uint16_t *y,
+                                           q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_common(hidden, w, y, T, H, eps))
+        return st;
+    if (V <= 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "embedding weight dimensions must be positive");
+    if (T == 0)
+        return Q3K_OK;
+    if (ids == nullptr || table == nullptr)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "embedding received a null pointer");
+    if (!aligned_to(ids, 4) || !aligned_to(table, 2))
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "embedding pointers must be aligned to their element size");
+    if (V > INT64_MAX / H)
+        return set_error(Q3K_ERR_OVERFLOW, "embedding size overflows");
+    const RowMap map{0, 1, ids, table, V};
+    return rms_dispatch<kGatherNorm>(hidden, nullptr, w, y, T, H, eps, map, reinterpret_cast<hipStream_t>(stream),
+                                     "embedding_rms_norm");
 }

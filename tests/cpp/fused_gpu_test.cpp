@@ -4,9 +4,12 @@
 #include "gpu_util.hpp"
 #include "qwen3/model/non_gemm_layer.h"
 #include "qwen3/ops/elementwise.h"
+#include "qwen3/ops/embedding.h"
 #include "qwen3/ops/fused.h"
 #include "qwen3/ops/rms_norm.h"
 #include "qwen3/ops/rope.h"
+
+#include <algorithm>
 
 using qwen3::DType;
 using qwen3::Shape;
@@ -86,6 +89,70 @@ namespace
                                               "float32 norm weight accepted");
     }
 
+    // Rows [b, S-1, :] of a [B, S, H] host copy, as select_last_token_hidden returns them.
+    std::vector<uint16_t> last_rows(const std::vector<uint16_t> &all, std::int64_t b, std::int64_t s, std::int64_t h)
+    {
+        std::vector<uint16_t> out;
+        for (std::int64_t i = 0; i < b; ++i)
+            out.insert(out.end(), all.begin() + ((i * s + s - 1) * h), all.begin() + ((i * s + s) * h));
+        return out;
+    }
+
+    void embedding_rms_norm_case()
+    {
+        constexpr std::int64_t V = 300;
+        Tensor table = gpu_values(Shape{V, H}, 30), w = gpu_values(Shape{H}, 31, 0.1f, 1.0f);
+        std::vector<int32_t> ids(B * S);
+        for (std::size_t i = 0; i < ids.size(); ++i)
+            ids[i] = static_cast<int32_t>((i * 7919) % V);
+        ids[3] = -1;
+        ids[5] = static_cast<int32_t>(V);
+        Tensor gid = test::to_gpu(ids, Shape{B, S}, DType::Int32);
+        const auto fused = qwen3::ops::embedding_rms_norm(gid, table, w, kEps);
+        require(fused.hidden.shape() == (Shape{B, S, H}) && fused.normalized.shape() == (Shape{B, S, H}),
+                "embedding_rms_norm shapes");
+        Tensor hidden = qwen3::ops::embedding_lookup(gid, table);
+        Tensor normalized = qwen3::ops::rms_norm(hidden, w, kEps);
+        require(test::to_host<uint16_t>(fused.hidden) == test::to_host<uint16_t>(hidden), "gather equals embedding_lookup");
+        require(test::to_host<uint16_t>(fused.normalized) == test::to_host<uint16_t>(normalized),
+                "embedding_rms_norm equals embedding_lookup + rms_norm");
+        require_throws<std::invalid_argument>([&] { (void)qwen3::ops::embedding_rms_norm(gid, table, table, kEps); },
+                                              "two-dimensional norm weight accepted");
+        require_throws<std::invalid_argument>(
+            [&] { (void)qwen3::ops::embedding_rms_norm(gid, table, gpu_values(Shape{H + 8}, 32), kEps); },
+            "norm weight of the wrong size accepted");
+    }
+
+    void last_token_case()
+    {
+        Tensor h1 = gpu_values(Shape{B, S, H}, 40), h2 = gpu_values(Shape{B, S, H}, 40);
+        Tensor d = gpu_values(Shape{B, S, H}, 41), w = gpu_values(Shape{H}, 42, 0.1f, 1.0f);
+        const auto h0 = test::to_host<uint16_t>(h1);
+        Tensor y = qwen3::ops::rms_norm_last_token(h1, w, kEps);
+        require(y.shape() == (Shape{B, H}), "last-token norm shape");
+        const auto full = test::to_host<uint16_t>(qwen3::ops::rms_norm(h1, w, kEps));
+        require(test::to_host<uint16_t>(y) == last_rows(full, B, S, H),
+                "rms_norm_last_token equals the last rows of rms_norm");
+
+        Tensor ya = qwen3::ops::add_rms_norm_last_token(h1, d, w, kEps);
+        qwen3::ops::add_inplace(h2, d);
+        const auto summed = test::to_host<uint16_t>(h2);
+        const auto full_a = test::to_host<uint16_t>(qwen3::ops::rms_norm(h2, w, kEps));
+        require(test::to_host<uint16_t>(ya) == last_rows(full_a, B, S, H),
+                "add_rms_norm_last_token equals the last rows of add_inplace + rms_norm");
+        const auto got = test::to_host<uint16_t>(h1);
+        for (std::int64_t b = 0; b < B; ++b)
+            for (std::int64_t s = 0; s < S; ++s)
+            {
+                const auto &want = s == S - 1 ? summed : h0;
+                const std::int64_t at = (b * S + s) * H;
+                require(std::equal(got.begin() + at, got.begin() + at + H, want.begin() + at),
+                        "residual: last rows updated, earlier rows untouched");
+            }
+        require_throws<std::invalid_argument>([&] { (void)qwen3::ops::rms_norm_last_token(w, w, kEps); },
+                                              "rank-1 hidden states accepted");
+    }
+
     void layer_chain_case()
     {
         Tensor cache = qwen3::ops::build_rope_cache(S, static_cast<std::int32_t>(D), 1.0e6f, qwen3::Device::cuda(0));
@@ -113,6 +180,8 @@ namespace
         const int before = test::current_device();
         add_rms_norm_case();
         qk_norm_rope_case();
+        embedding_rms_norm_case();
+        last_token_case();
         layer_chain_case();
         require(test::current_device() == before, "a fused op changed the current device");
     }

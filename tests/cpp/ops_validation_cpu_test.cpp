@@ -36,6 +36,14 @@ static void body()
     require_throws<std::invalid_argument>([&] { (void)qwen3::ops::embedding_lookup(ids, table); }, "embedding host tensors");
     require_throws<std::invalid_argument>([&] { (void)qwen3::ops::embedding_lookup(table, table); }, "embedding bf16 ids");
     require_throws<std::invalid_argument>([&] { (void)qwen3::ops::add_rms_norm(x, x, w, 1e-6f); }, "add_rms_norm host tensors");
+    require_throws<std::invalid_argument>([&] { (void)qwen3::ops::embedding_rms_norm(ids, table, w, 1e-6f); },
+                                          "embedding_rms_norm host tensors");
+    require_throws<std::invalid_argument>([&] { (void)qwen3::ops::rms_norm_last_token(x, w, 1e-6f); },
+                                          "last-token norm host tensors");
+    require_throws<std::invalid_argument>([&] { (void)qwen3::ops::rms_norm_last_token(f, w, 1e-6f); },
+                                          "last-token norm float32 input");
+    require_throws<std::invalid_argument>([&] { (void)qwen3::ops::add_rms_norm_last_token(x, x, w, 1e-6f); },
+                                          "last-token add norm host tensors");
 
     Tensor cache = qwen3::ops::build_rope_cache(16, 8, 1.0e6f, cpu);
     require(cache.shape() == (Shape{16, 4, 2}) && cache.dtype() == DType::Float32 && cache.device().is_cpu(),

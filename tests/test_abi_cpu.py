@@ -106,3 +106,17 @@ def test_error_string_is_thread_local(q3k):
     t.join()
     assert seen["msg"] == "no error"
     assert "normalized size" in lib.q3k_last_error_string().decode()
+
+
+def test_caller_fusion_argument_errors(q3k):
+    IA, OV = q3k.Q3K_ERR_INVALID_ARGUMENT, q3k.Q3K_ERR_OVERFLOW
+    fake = 256
+    _expect(q3k.rms_norm_rows, ValueError, IA, fake, fake, fake, 4, -1, 8, 1024, 1e-6)
+    _expect(q3k.rms_norm_rows, ValueError, IA, fake, fake, fake, 4, 0, -8, 1024, 1e-6)
+    _expect(q3k.add_rms_norm_rows, OverflowError, OV, fake, fake, fake, fake, 4, 2**61, 1, 1024, 1e-6)
+    _expect(q3k.add_rms_norm_rows, ValueError, IA, fake, None, fake, fake, 4, 0, 1, 1024, 1e-6)
+    _expect(q3k.embedding_rms_norm, ValueError, IA, fake, 4, fake, 0, 1024, fake, 1e-6, fake, fake)
+    _expect(q3k.embedding_rms_norm, ValueError, IA, None, 4, fake, 10, 1024, fake, 1e-6, fake, fake)
+    _expect(q3k.embedding_rms_norm, ValueError, IA, fake, 4, fake, 10, 1024, fake, 0.0, fake, fake)
+    q3k.rms_norm_rows(None, None, None, 0, 0, 1, 1024, 1e-6)
+    q3k.embedding_rms_norm(None, 0, None, 10, 1024, None, 1e-6, None, None)

@@ -313,3 +313,56 @@ def test_fused_equals_unfused_on_gpu(q3k, hip, synth):
     nk = run_rms(q3k, hip, k, kw)
     check_exact("qk_norm_rope vs rms_norm + rope (q)", fq, run_rope(q3k, hip, nq, 1, T, Hq, D, cache))
     check_exact("qk_norm_rope vs rms_norm + rope (k)", fk, run_rope(q3k, hip, nk, 1, T, Hkv, D, cache))
+
+
+# ---------------------------------------------------------------- caller fusions
+
+@pytest.mark.parametrize("V,H,T,offset", [(1000, 1024, 77, 0), (500, 4096, 40, 0), (300, 5120, 9, 0),
+                                          (64, 8192, 5, 0), (50, 12, 7, 0), (100, 1024, 10, 2), (64, 128, 33, 0)])
+def test_embedding_rms_norm(q3k, hip, oracle, synth, V, H, T, offset):
+    """Gather + first input norm: model.cpp:118 -> decoder_layer.cpp:72."""
+    name = f"embedding_rms_norm V={V} H={H} T={T} offset={offset}"
+    announce(name)
+    table = synth.normal_bf16(120, H, (V, H))
+    w = synth.normal_bf16(121, H, (H,), mean=1.0, std=0.1)
+    ids = synth.token_ids(122, T, (T,), V)
+    ids[:2] = [-3, V][:min(2, T)]
+    I, Tb, W = Guarded(hip, ids), Guarded(hip, table, offset=offset), Guarded(hip, w, offset=offset)
+    Hd, Y = Guarded(hip, nbytes=T * H * 2, offset=offset), Guarded(hip, nbytes=T * H * 2, offset=offset)
+    q3k.embedding_rms_norm(I, T, Tb, V, H, W, EPS, Hd, Y)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (I, Tb, W, Hd, Y))
+    emb = oracle.embedding(ids, table)
+    check_exact(name + " hidden", Hd.get(np.uint16, (T, H)), emb)
+    prim, lo, hi = oracle.rms_norm(emb, w, EPS)
+    check_band(oracle, name, Y.get(np.uint16, (T, H)), prim, lo, hi)
+
+
+@pytest.mark.parametrize("B,S,H,add,offset", [(4, 33, 4096, True, 0), (4, 33, 4096, False, 0), (2, 17, 5120, True, 0),
+                                              (3, 5, 1024, False, 0), (64, 1, 4096, True, 0), (2, 9, 257, True, 0),
+                                              (3, 7, 1024, True, 2)])
+def test_last_token_norm(q3k, hip, oracle, synth, B, S, H, add, offset):
+    """Final norm of the last token of each sequence: model.cpp:146 + lm_head.cpp:123-181."""
+    name = f"last_token_norm B={B} S={S} H={H} add={add} offset={offset}"
+    announce(name)
+    h = synth.normal_bf16(123, H, (B, S, H))
+    d = synth.normal_bf16(124, H, (B, S, H))
+    w = synth.normal_bf16(125, H, (H,), mean=1.0, std=0.1)
+    Hb, Db, W = Guarded(hip, h, offset=offset), Guarded(hip, d, offset=offset), Guarded(hip, w, offset=offset)
+    Y = Guarded(hip, nbytes=B * H * 2, offset=offset)
+    if add:
+        q3k.add_rms_norm_rows(Hb, Db, W, Y, B, S - 1, S, H, EPS)
+    else:
+        q3k.rms_norm_rows(Hb, W, Y, B, S - 1, S, H, EPS)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (Hb, Db, W, Y))
+    h_got = Hb.get(np.uint16, (B, S, H))
+    last_h = h[:, -1, :]
+    expect_h = h.copy()
+    if add:
+        expect_h[:, -1, :] = oracle.add_inplace(last_h, d[:, -1, :])
+        _, prim, lo, hi = oracle.add_rms_norm(last_h, d[:, -1, :], w, EPS)
+    else:
+        prim, lo, hi = oracle.rms_norm(last_h, w, EPS)
+    check_exact(name + " residual (only last rows change)", h_got, expect_h)
+    check_band(oracle, name, Y.get(np.uint16, (B, H)), prim, lo, hi)
