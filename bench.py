@@ -330,6 +330,44 @@ def main():
         extras["copy_ceiling_GB/s"] = round(2 * nb / (ms_cp * 1e-3) / 1e9, 1)
         src.free()
         dst.free()
+        # Q/K norm + RoPE + KV-cache append (self_attention.cpp:147-156) fused, against qk_norm_rope followed by
+        # the append; the cache holds the whole sequence (capacity S), written at cached length 0
+        print("[bench] timing KV append", file=sys.stderr, flush=True)
+        kv_row = c.heads_kv * D * 2
+        kv_set_bytes = T * c.heads_q * D * 2 + 4 * T * kv_row
+        kv_sets = []
+        for i in range(-(-MIN_CYCLE_BYTES // kv_set_bytes)):
+            src = sets[i % len(sets)]
+            e = {"q": hip.DeviceBuffer(src["q"].nbytes), "k": hip.DeviceBuffer(src["k"].nbytes),
+                 "v": hip.DeviceBuffer(T * kv_row), "kc": hip.DeviceBuffer(T * kv_row), "vc": hip.DeviceBuffer(T * kv_row)}
+            e["q"].copy_from(src["q"])
+            e["k"].copy_from(src["k"])
+            e["v"].copy_from(src["k"])
+            kv_sets.append(e)
+        b0 = sets[0]
+        ms_kv = time_chain(hip, stream, kv_sets, lambda e: [
+            ("qk_norm_rope_kv_append", lambda: q3k.qk_norm_rope_kv_append(
+                e["q"], e["k"], e["v"], b0["qw"], b0["kw"], c.batch, c.seq, c.heads_q, c.heads_kv, D, EPS, b0["cache"],
+                c.max_pos, 0, e["kc"], e["vc"], c.seq, 0, None, stream))], max(20, len(kv_sets)), 3)
+        ms_kv_pair = time_chain(hip, stream, kv_sets, lambda e: [
+            ("qk_norm_rope", lambda: q3k.qk_norm_rope(e["q"], e["k"], b0["qw"], b0["kw"], c.batch, c.seq, c.heads_q,
+                                                      c.heads_kv, D, EPS, b0["cache"], c.max_pos, 0, None, stream)),
+            ("kv_append", lambda: q3k.kv_append(e["k"], e["v"], e["kc"], e["vc"], c.batch, c.seq, kv_row, c.seq, 0,
+                                                stream))], max(20, len(kv_sets)), 3)
+        ms_append = time_chain(hip, stream, kv_sets, lambda e: [
+            ("kv_append", lambda: q3k.kv_append(e["k"], e["v"], e["kc"], e["vc"], c.batch, c.seq, kv_row, c.seq, 0,
+                                                stream))], max(20, len(kv_sets)), 3)
+        U = c.distinct_positions()
+        kvb = configs.bytes_qk_norm_rope_kv_append(T, c.heads_q, c.heads_kv, D, U)
+        ab = configs.bytes_kv_append(T, c.heads_kv, D)
+        extras["qk_norm_rope_kv_append"] = {"ms": round(ms_kv, 5), "bytes": kvb,
+                                            "GB/s": round(kvb / (ms_kv * 1e-3) / 1e9, 1),
+                                            "unfused_ms": round(ms_kv_pair, 5),
+                                            "fused_speedup": round(ms_kv_pair / ms_kv, 3)}
+        extras["kv_append"] = {"ms": round(ms_append, 5), "bytes": ab, "GB/s": round(ab / (ms_append * 1e-3) / 1e9, 1)}
+        for e in kv_sets:
+            for buf in e.values():
+                buf.free()
         if "embedding" in c.ops:
             print("[bench] timing embedding", file=sys.stderr, flush=True)
             for s in sets[1:]:

@@ -169,6 +169,39 @@ Q3K_API int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k,
                           const int32_t *positions, q3k_stream_t stream);
 
 /*
+ * KV-cache append: K and V [B, S, row_bytes] (contiguous) are copied to rows
+ * start .. start + S - 1 of batch rows 0 .. B - 1 of one layer's cache
+ * [batch_cap, seq_cap, row_bytes] (key_cache / value_cache point at the
+ * layer; the caller guarantees B <= batch_cap).  Bytes are copied unchanged
+ * (bf16 or fp32 caches).  start + S > seq_cap is Q3K_ERR_OUT_OF_RANGE.
+ * Replaces the two cudaMemcpy2DAsync of qwen3::KvCache::append,
+ * src/model/kv_cache.cpp:76-204 (capacity check :121-125).
+ */
+Q3K_API int q3k_kv_append(const void *key, const void *value, void *key_cache,
+                  void *value_cache, int64_t B, int64_t S, int64_t row_bytes,
+                  int64_t seq_cap, int64_t start, q3k_stream_t stream);
+
+/*
+ * Fused Q/K RMSNorm + RoPE + KV-cache append: Q is normalised and rotated in
+ * place as by q3k_qk_norm_rope_bf16; K is normalised and rotated straight
+ * into the bf16 key cache and V copied into the value cache, at the rows
+ * q3k_kv_append would use (cache_start = the layer's cached length).  K and V
+ * are only read.  The results equal q3k_qk_norm_rope_bf16 followed by
+ * q3k_kv_append bit for bit.  Cache rows must not overlap q, k or v.
+ * Replaces the sequence rms_norm(q) -> rms_norm(k) -> apply_rope_inplace ->
+ * kv_cache.append at src/model/self_attention.cpp:147-156
+ * (src/model/kv_cache.cpp:76-204).
+ */
+Q3K_API int q3k_qk_norm_rope_kv_append_bf16(uint16_t *q, const uint16_t *k,
+                          const uint16_t *v, const uint16_t *qw,
+                          const uint16_t *kw, int64_t B, int64_t S,
+                          int32_t Hq, int32_t Hkv, int32_t D, float eps,
+                          const float *cache, int64_t P, int64_t start,
+                          const int32_t *positions, uint16_t *k_cache,
+                          uint16_t *v_cache, int64_t seq_cap,
+                          int64_t cache_start, q3k_stream_t stream);
+
+/*
  * Host-side RoPE table: cache[p, i, 0] = (float)cos(p * theta^(-2i/D)),
  * cache[p, i, 1] = (float)sin(...), evaluated in double, for p in [0, P),
  * i in [0, D/2).  Writes P * D floats to host memory.  Same recipe and

@@ -525,3 +525,17 @@ void q3o_compare_band(const uint16_t *got, const uint16_t *primary, const uint16
         }
     }
 }
+
+/* ---- KV-cache append: src/model/kv_cache.cpp:147-185 ------------------- */
+
+void q3o_kv_append(const void *k, const void *v, void *kc, void *vc, int64_t B, int64_t S, int64_t row_bytes,
+                   int64_t seq_cap, int64_t start)
+{
+    const int64_t width = S * row_bytes;          /* source pitch = copy width */
+    const int64_t dst_pitch = seq_cap * row_bytes; /* one batch row of the cache */
+    for (int64_t b = 0; b < B; ++b)
+    {
+        memcpy((char *)kc + b * dst_pitch + start * row_bytes, (const char *)k + b * width, (size_t)width);
+        memcpy((char *)vc + b * dst_pitch + start * row_bytes, (const char *)v + b * width, (size_t)width);
+    }
+}

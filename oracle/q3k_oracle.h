@@ -71,6 +71,13 @@ int q3o_qk_norm_rope(uint16_t *x, const uint16_t *w, int64_t B, int64_t S, int32
                      float eps, const float *cache, int64_t P, int64_t start,
                      const int32_t *positions, uint16_t *lo, uint16_t *hi, int nthreads);
 
+/* KV-cache append, src/model/kv_cache.cpp:147-185: two 2-D copies of B rows
+ * of S * row_bytes bytes, source pitch S * row_bytes, destination pitch
+ * seq_cap * row_bytes, starting at row start of the layer block
+ * [batch_cap, seq_cap, row_bytes] that kc / vc point at.  Bit-exact. */
+void q3o_kv_append(const void *k, const void *v, void *kc, void *vc, int64_t B, int64_t S, int64_t row_bytes,
+                   int64_t seq_cap, int64_t start);
+
 /* Comparison of kernel output against (primary, lo, hi).
  * stats[0] = elements, [1] = failures (outside [lo-1, hi+1]),
  * [2] = first failing index or -1, [3] = ambiguous elements (lo != hi),

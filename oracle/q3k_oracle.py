@@ -34,6 +34,7 @@ def lib() -> ctypes.CDLL:
             "q3o_build_rope_cache": ([_i64, _i32, _f32, _p], _int),
             "q3o_rope": ([_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p, _p, _int], _int),
             "q3o_qk_norm_rope": ([_p, _p, _i64, _i64, _i32, _i32, _f32, _p, _i64, _i64, _p, _p, _p, _int], _int),
+            "q3o_kv_append": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64], None),
             "q3o_compare_band": ([_p, _p, _p, _p, _i64, _p], None),
             "q3o_ulp_distance": ([ctypes.c_uint16, ctypes.c_uint16], ctypes.c_int32),
             "q3o_bf16_from_f32": ([_f32], ctypes.c_uint16),
@@ -145,6 +146,19 @@ def qk_norm_rope(x, w, B, S, heads, D, eps, cache, start=0, positions=None, band
     if st != 0:
         raise ValueError("bad Q/K norm + RoPE arguments")
     return x, lo, hi
+
+
+def kv_append(k, v, k_cache, v_cache, start):
+    """k, v [B, S, row] into copies of the layer caches [batch_cap, seq_cap, row] at row `start`."""
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    kc = np.array(k_cache, copy=True, order="C")
+    vc = np.array(v_cache, copy=True, order="C")
+    B, S = k.shape[0], k.shape[1]
+    row_bytes = k[0, 0].nbytes
+    seq_cap = kc.shape[1]
+    lib().q3o_kv_append(_ptr(k), _ptr(v), _ptr(kc), _ptr(vc), B, S, row_bytes, seq_cap, start)
+    return kc, vc
 
 
 def compare(got, primary, lo=None, hi=None) -> dict:

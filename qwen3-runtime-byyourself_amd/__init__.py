@@ -80,6 +80,9 @@ SIGNATURES = {
     "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
+    "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
+    "q3k_qk_norm_rope_kv_append_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p,
+                                        _p, _p, _i64, _i64, _p],
     "q3k_build_rope_cache_f32": [_p, _i64, _i32, _f32],
     "q3k_bench_copy_u128": [_p, _p, _i64, _p],
 }
@@ -178,6 +181,18 @@ def rope(x, B, S, heads, D, cache, P, start, positions=None, stream=None):
 def qk_norm_rope(q, k, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, positions=None, stream=None):
     _check(load().q3k_qk_norm_rope_bf16(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw), B, S, Hq, Hkv, D, eps,
                                         _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
+
+
+def kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, start, stream=None):
+    _check(load().q3k_kv_append(_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), B, S, row_bytes, seq_cap, start,
+                                _ptr(stream)))
+
+
+def qk_norm_rope_kv_append(q, k, v, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, k_cache, v_cache, seq_cap,
+                           cache_start, positions=None, stream=None):
+    _check(load().q3k_qk_norm_rope_kv_append_bf16(_ptr(q), _ptr(k), _ptr(v), _ptr(qw), _ptr(kw), B, S, Hq, Hkv, D,
+                                                  eps, _ptr(cache), P, start, _ptr(positions), _ptr(k_cache),
+                                                  _ptr(v_cache), seq_cap, cache_start, _ptr(stream)))
 
 
 def build_rope_cache(P: int, D: int, theta: float):

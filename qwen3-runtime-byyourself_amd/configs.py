@@ -73,6 +73,16 @@ def bytes_qk_norm_rope(T, Hq, Hkv, D, U):
     return 2 * T * (Hq + Hkv) * D * 2 + U * (D // 2) * 2 * 4 + 2 * 2 * D
 
 
+def bytes_kv_append(T, Hkv, D):
+    """K and V rows read once and written once into the cache."""
+    return 2 * 2 * T * Hkv * D * 2
+
+
+def bytes_qk_norm_rope_kv_append(T, Hq, Hkv, D, U):
+    """Q in place; K read and written to the cache; V read and copied; table and weights once."""
+    return 2 * T * (Hq + 2 * Hkv) * D * 2 + U * (D // 2) * 2 * 4 + 2 * 2 * D
+
+
 def bytes_silu_mul(T, I):
     return 3 * T * I * 2
 

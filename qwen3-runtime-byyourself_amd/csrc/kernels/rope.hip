@@ -24,6 +24,11 @@ namespace q3k
     // Declared in rms_norm.hip: the generic RMSNorm used by the fused op's
     // fallback path.
     int launch_rms_generic(uint16_t *x, const uint16_t *w, int64_t rows, int64_t n, float eps, hipStream_t stream);
+    // Declared in kv_cache.hip: the KV-cache append's checks and its copy kernel.
+    int validate_kv_append(const void *k, const void *v, const void *kc, const void *vc, int64_t B, int64_t S,
+                           int64_t row_bytes, int64_t seq_cap, int64_t start);
+    void launch_kv_append(const void *k, const void *v, void *kc, void *vc, int64_t B, int64_t S, int64_t row_bytes,
+                          int64_t seq_cap, int64_t start, hipStream_t stream);
 
     namespace
     {
@@ -58,31 +63,49 @@ namespace q3k
             return (pos >= 0 && pos < rs.table_positions) ? pos : -1;
         }
 
-        // One wave = 4 * HG consecutive heads of one token (heads % (4 * HG)
-        // == 0): lane l of the wave works on heads head0 + l/16 + 4i, i < HG,
-        // elements 8(l%16) .. +7 of each.  The table row, the sign pattern and
-        // the norm weights depend only on the lane and the position, so they
-        // are loaded and unpacked once per wave.  head0 and the token are
-        // wave-uniform and below 2^31 (checked by the launcher).
-        template <bool NORM, int NTM, int HG>
-        __device__ __forceinline__ void rope_heads(uint16_t *base, const uint16_t *w, uint32_t head0, uint32_t heads,
-                                                   const RopeShape &rs, float eps)
+        // Where the K (and V) heads of the fused KV-cache append go: token
+        // t = b * S + s of the input lands in row b * seq_cap + cache_start + s
+        // of the layer's [batch_cap, seq_cap, Hkv, D] cache.  V is copied
+        // unchanged next to the roped K.
+        struct KvDest
         {
-            constexpr int kVecPerHead = kHeadDim / 8;
-            const int lane16 = threadIdx.x % 16;
-            const uint32_t token = head0 / heads;
-            const int64_t pos = token_position(rs, token);
+            const uint16_t *v;
+            uint16_t *k_cache;
+            uint16_t *v_cache;
+            int64_t seq_cap;
+            int64_t cache_start;
+        };
 
-            Vec8 *hv = reinterpret_cast<Vec8 *>(base) +
-                       (static_cast<int64_t>(head0) + (threadIdx.x % kWave) / 16) * kVecPerHead + lane16;
+        constexpr int kVecPerHead = kHeadDim / 8;
+        constexpr int kHeadStride = kHeadsPerWave * kVecPerHead;  // Vec8s between a lane's heads
+
+        // One wave = 4 * HG consecutive heads of one token (heads % (4 * HG)
+        // == 0): lane l of the wave works on heads l/16 + 4i, i < HG, of
+        // `src`/`dst` (already offset to the wave's first head and the lane's
+        // vector), elements 8(l%16) .. +7 of each.  The table row, the sign
+        // pattern and the norm weights depend only on the lane and the
+        // position, so they are loaded and unpacked once per wave.  With
+        // COPY_V the wave also moves the matching V heads from vsrc to vdst.
+        template <bool NORM, int NTM, int HG, bool COPY_V>
+        __device__ __forceinline__ void rope_heads(const Vec8 *src, Vec8 *dst, const Vec8 *vsrc, Vec8 *vdst,
+                                                   const uint16_t *w, const float *table, int64_t pos, float eps)
+        {
+            const int lane16 = threadIdx.x % 16;
             // Raised wave priority while the head loads are issued gets them
             // to the memory system ahead of other waves' arithmetic (+5%
             // measured at the model's shapes).
             Vec8 x[HG];
+            Vec8 xv[COPY_V ? HG : 1];
             __builtin_amdgcn_s_setprio(3);
 #pragma unroll
             for (int i = 0; i < HG; ++i)
-                x[i] = load8<nt_load(NTM)>(hv + i * kHeadsPerWave * kVecPerHead);
+                x[i] = load8<nt_load(NTM)>(src + i * kHeadStride);
+            if constexpr (COPY_V)
+            {
+#pragma unroll
+                for (int i = 0; i < HG; ++i)
+                    xv[i] = load8<nt_load(NTM)>(vsrc + i * kHeadStride);
+            }
             __builtin_amdgcn_s_setprio(0);
 
             if (pos < 0)
@@ -90,7 +113,13 @@ namespace q3k
                 const Vec8 nan = {{kNanPair, kNanPair, kNanPair, kNanPair}};
 #pragma unroll
                 for (int i = 0; i < HG; ++i)
-                    store8<nt_store(NTM)>(hv + i * kHeadsPerWave * kVecPerHead, nan);
+                    store8<nt_store(NTM)>(dst + i * kHeadStride, nan);
+                if constexpr (COPY_V)
+                {
+#pragma unroll
+                    for (int i = 0; i < HG; ++i)
+                        store8<nt_store(NTM)>(vdst + i * kHeadStride, xv[i]);
+                }
                 return;
             }
 
@@ -107,7 +136,7 @@ namespace q3k
             }
             // cos and sin of pairs 8(l%8) .. +7; first-half lanes use -sin so
             // that both halves compute own * cos + partner * sin'.
-            const F4 *crow = reinterpret_cast<const F4 *>(rs.cache + (pos * kHalf + (lane16 % 8) * 8) * 2);
+            const F4 *crow = reinterpret_cast<const F4 *>(table + (pos * kHalf + (lane16 % 8) * 8) * 2);
             const uint32_t sign = lane16 < 8 ? 0x80000000u : 0u;
             float cs[8], sn[8];
 #pragma unroll
@@ -159,28 +188,66 @@ namespace q3k
                     const float b1 = dpp_f<kDppRowRor8>(v[2 * j + 1]) * sn[2 * j + 1];
                     r.d[j] = pack_rne(a0 + b0, a1 + b1);
                 }
-                store8<nt_store(NTM)>(hv + i * kHeadsPerWave * kVecPerHead, r);
+                store8<nt_store(NTM)>(dst + i * kHeadStride, r);
+            }
+            if constexpr (COPY_V)
+            {
+#pragma unroll
+                for (int i = 0; i < HG; ++i)
+                    store8<nt_store(NTM)>(vdst + i * kHeadStride, xv[i]);
             }
         }
 
-        // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with HGK.
-        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP>
+        // The lane's vector of head `head` (counted over the whole tensor) of
+        // a [tokens, heads, 128] tensor.
+        __device__ __forceinline__ int64_t lane_vec(int64_t head)
+        {
+            return (head + (threadIdx.x % kWave) / 16) * kVecPerHead + threadIdx.x % 16;
+        }
+
+        // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with
+        // HGK.  Q is rewritten in place; K in place too, or with KV into the
+        // cache rows given by `kv` (k itself is then only read).  Heads and
+        // tokens are wave-uniform and below 2^31 (checked by the launcher).
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
             int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
-            RopeShape rs, float eps)
+            RopeShape rs, float eps, KvDest kv)
         {
             const int64_t wave = static_cast<int64_t>(tile_index<REMAP>(blockIdx.x, gridDim.x)) * kWavesPerBlock +
                                  __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             if (wave >= total_waves)
                 return;
             if (wave < q_waves)
-                rope_heads<NORM, NTM, HGQ>(q, qw, static_cast<uint32_t>(wave * kHeadsPerWave * HGQ),
-                                           static_cast<uint32_t>(heads_q), rs, eps);
+            {
+                const uint32_t head0 = static_cast<uint32_t>(wave * kHeadsPerWave * HGQ);
+                const uint32_t token = head0 / static_cast<uint32_t>(heads_q);
+                Vec8 *p = reinterpret_cast<Vec8 *>(q) + lane_vec(head0);
+                rope_heads<NORM, NTM, HGQ, false>(p, p, nullptr, nullptr, qw, rs.cache, token_position(rs, token),
+                                                  eps);
+                return;
+            }
+            const uint32_t head0 = static_cast<uint32_t>((wave - q_waves) * kHeadsPerWave * HGK);
+            const uint32_t token = head0 / static_cast<uint32_t>(heads_k);
+            const int64_t pos = token_position(rs, token);
+            Vec8 *src = reinterpret_cast<Vec8 *>(k) + lane_vec(head0);
+            if constexpr (KV)
+            {
+                const uint32_t seq = static_cast<uint32_t>(rs.seq);
+                const uint32_t b = token / seq;
+                const int64_t row = static_cast<int64_t>(b) * kv.seq_cap + kv.cache_start + (token - b * seq);
+                const int64_t dst_head = row * heads_k + (head0 - token * static_cast<uint32_t>(heads_k));
+                rope_heads<NORM, NTM, HGK, true>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + lane_vec(dst_head),
+                                                 reinterpret_cast<const Vec8 *>(kv.v) + lane_vec(head0),
+                                                 reinterpret_cast<Vec8 *>(kv.v_cache) + lane_vec(dst_head), kw,
+                                                 rs.cache, pos, eps);
+            }
             else
-                rope_heads<NORM, NTM, HGK>(k, kw, static_cast<uint32_t>((wave - q_waves) * kHeadsPerWave * HGK),
-                                           static_cast<uint32_t>(heads_k), rs, eps);
+            {
+                rope_heads<NORM, NTM, HGK, false>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
+            }
         }
 
         // Generic RoPE: one thread per (token, head, pair), any even head_dim.
@@ -269,36 +336,36 @@ namespace q3k
         // heads), else 2 (8 KV heads), else 1.
         int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
 
-        template <bool NORM, int HGQ, int HGK>
+        template <bool NORM, bool KV, int HGQ, int HGK>
         void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
-                             int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream)
+                             int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv, hipStream_t stream)
         {
             constexpr int NTM = NORM ? kNtmNormRope : kNtmRope;
             const int64_t q_waves = waves_for(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
-                q, k, qw, kw, hq, hk, q_waves, total, rs, eps);
+            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+                q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
-        template <bool NORM>
+        template <bool NORM, bool KV = false>
         void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
-                          int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream)
+                          int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream, const KvDest &kv = {})
         {
             const int gq = heads_per_lane(hq);
             const int gk = k == nullptr ? gq : heads_per_lane(hk);
             const int key = gq * 10 + gk;
             switch (key)
             {
-            case 44: launch_heads_hg<NORM, 4, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 42: launch_heads_hg<NORM, 4, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 41: launch_heads_hg<NORM, 4, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 24: launch_heads_hg<NORM, 2, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 22: launch_heads_hg<NORM, 2, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 21: launch_heads_hg<NORM, 2, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 14: launch_heads_hg<NORM, 1, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            case 12: launch_heads_hg<NORM, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
-            default: launch_heads_hg<NORM, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, stream); break;
+            case 44: launch_heads_hg<NORM, KV, 4, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 42: launch_heads_hg<NORM, KV, 4, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 41: launch_heads_hg<NORM, KV, 4, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 24: launch_heads_hg<NORM, KV, 2, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 22: launch_heads_hg<NORM, KV, 2, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 21: launch_heads_hg<NORM, KV, 2, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 14: launch_heads_hg<NORM, KV, 1, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 12: launch_heads_hg<NORM, KV, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            default: launch_heads_hg<NORM, KV, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
             }
         }
 
@@ -362,4 +429,55 @@ extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *q
     launch_generic_rope(q, Hq, D, rs, s);
     launch_generic_rope(k, Hkv, D, rs, s);
     return check_launch("qk_norm_rope (generic)");
+}
+
+extern "C" int q3k_qk_norm_rope_kv_append_bf16(uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                               const uint16_t *qw, const uint16_t *kw, int64_t B, int64_t S,
+                                               int32_t Hq, int32_t Hkv, int32_t D, float eps, const float *cache,
+                                               int64_t P, int64_t start, const int32_t *positions,
+                                               uint16_t *k_cache, uint16_t *v_cache, int64_t seq_cap,
+                                               int64_t cache_start, q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_rope(q, B, S, Hq, D, cache, P, start, positions))
+        return st;
+    if (const int st = validate_rope(k, B, S, Hkv, D, cache, P, start, positions))
+        return st;
+    if (!(eps > 0.0f) || eps == __builtin_huge_valf())
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm epsilon must be finite and positive");
+    const int64_t row_bytes = static_cast<int64_t>(Hkv) * D * 2;
+    if (const int st = validate_kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, cache_start))
+        return st;
+    const int64_t tokens = B * S;
+    if (tokens == 0)
+        return Q3K_OK;
+    if (qw == nullptr || kw == nullptr)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "Q/K norm weight pointer is null");
+    if (!aligned_to(qw, 2) || !aligned_to(kw, 2) || !aligned_to(v, 2) || !aligned_to(k_cache, 2) ||
+        !aligned_to(v_cache, 2))
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "bf16 pointers must be 2-byte aligned");
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const RopeShape rs{tokens, S, P, start, positions, cache};
+    if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) && aligned16(v) &&
+        aligned16(k_cache) && aligned16(v_cache) && grid_ok(tokens, Hq + Hkv))
+    {
+        const KvDest kv{v, k_cache, v_cache, seq_cap, cache_start};
+        launch_heads<true, true>(q, const_cast<uint16_t *>(k), qw, kw, Hq, Hkv, tokens, rs, eps, s, kv);
+        return check_launch("qk_norm_rope_kv_append");
+    }
+    // Generic path: copy K and V into the cache, then norm and rotate the
+    // cache rows of each sequence in place; Q as in qk_norm_rope.
+    launch_kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, cache_start, s);
+    int st = launch_rms_generic(q, qw, tokens * Hq, D, eps, s);
+    for (int64_t b = 0; st == Q3K_OK && b < B; ++b)
+        st = launch_rms_generic(k_cache + (b * seq_cap + cache_start) * Hkv * D, kw, S * Hkv, D, eps, s);
+    if (st != Q3K_OK)
+        return st;
+    launch_generic_rope(q, Hq, D, rs, s);
+    for (int64_t b = 0; b < B; ++b)
+    {
+        const RopeShape rb{S, S, P, start, positions == nullptr ? nullptr : positions + b * S, cache};
+        launch_generic_rope(k_cache + (b * seq_cap + cache_start) * Hkv * D, Hkv, D, rb, s);
+    }
+    return check_launch("qk_norm_rope_kv_append (generic)");
 }

@@ -3,6 +3,7 @@
 // checks, exception types and order); the table comes from the C ABI's host
 // builder (the recipe of src/ops/rope.cu:250-303).
 #include "qwen3/ops/fused.h"
+#include "qwen3/ops/kv_append.h"
 #include "qwen3/ops/rope.h"
 
 #include "ops_common.hpp"
@@ -166,5 +167,30 @@ namespace qwen3::ops
         validate_positions(query, positions);
         run_qk_norm_rope(query, key, q_weight, k_weight, epsilon, rope_cache, num_query_heads, num_key_value_heads, 0,
                          static_cast<const int32_t *>(positions.data()));
+    }
+
+    void qk_norm_rope_kv_append(Tensor &query, const Tensor &key, const Tensor &value, const Tensor &q_weight,
+                                const Tensor &k_weight, float epsilon, const Tensor &rope_cache,
+                                std::int32_t num_query_heads, std::int32_t num_key_value_heads,
+                                std::int64_t start_position, KvCache &kv_cache, std::int32_t layer_index)
+    {
+        validate_rope_tensors(query, key, rope_cache, num_query_heads, num_key_value_heads);
+        validate_norm_weights(query, rope_cache, q_weight, k_weight, epsilon);
+        validate_start(query, rope_cache, start_position);
+        detail::require(kv_cache.dtype() == DType::BFloat16, "fused KV append needs a BFloat16 cache");
+        const KvCache::AppendTarget target = kv_cache.prepare_append(layer_index, start_position, key, value);
+        const std::int64_t B = query.shape()[0], S = query.shape()[1];
+        const auto D = static_cast<std::int32_t>(rope_cache.shape()[1] * 2);
+        detail::require(D == kv_cache.head_dim() && num_key_value_heads == kv_cache.num_key_value_heads(),
+                        "KV cache head layout does not match the key");
+        detail::launch_on(query.device(), [&](q3k_stream_t stream) {
+            return q3k_qk_norm_rope_kv_append_bf16(
+                detail::bf16_ptr(query), detail::bf16_ptr(key), detail::bf16_ptr(value), detail::bf16_ptr(q_weight),
+                detail::bf16_ptr(k_weight), B, S, num_query_heads, num_key_value_heads, D, epsilon,
+                static_cast<const float *>(rope_cache.data()), rope_cache.shape()[0], start_position, nullptr,
+                static_cast<uint16_t *>(target.key_layer), static_cast<uint16_t *>(target.value_layer),
+                kv_cache.max_sequence_length(), start_position, stream);
+        });
+        kv_cache.commit_append(layer_index, start_position, target);
     }
 } // namespace qwen3::ops

@@ -3,6 +3,7 @@
 // device (reference src/ops/*: validate_* functions), and build_rope_cache
 // runs on the host.
 #include "qwen3/core/tensor.h"
+#include "qwen3/model/kv_cache.h"
 #include "qwen3/ops/elementwise.h"
 #include "qwen3/ops/embedding.h"
 #include "qwen3/ops/fused.h"
@@ -44,6 +45,16 @@ static void body()
                                           "last-token norm float32 input");
     require_throws<std::invalid_argument>([&] { (void)qwen3::ops::add_rms_norm_last_token(x, x, w, 1e-6f); },
                                           "last-token add norm host tensors");
+
+    // KvCache constructor checks (src/model/kv_cache.cpp:17-73)
+    require_throws<std::invalid_argument>([&] { qwen3::KvCache(0, 1, 4, 1, 8, DType::BFloat16, qwen3::Device::cuda(0)); },
+                                          "KV cache with zero layers");
+    require_throws<std::invalid_argument>([&] { qwen3::KvCache(1, 1, -4, 1, 8, DType::BFloat16, qwen3::Device::cuda(0)); },
+                                          "KV cache with negative capacity");
+    require_throws<std::invalid_argument>([&] { qwen3::KvCache(1, 1, 4, 1, 8, DType::Int32, qwen3::Device::cuda(0)); },
+                                          "KV cache with int32 dtype");
+    require_throws<std::invalid_argument>([&] { qwen3::KvCache(1, 1, 4, 1, 8, DType::BFloat16, cpu); },
+                                          "KV cache on the host");
 
     Tensor cache = qwen3::ops::build_rope_cache(16, 8, 1.0e6f, cpu);
     require(cache.shape() == (Shape{16, 4, 2}) && cache.dtype() == DType::Float32 && cache.device().is_cpu(),

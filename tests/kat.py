@@ -52,3 +52,23 @@ def embedding_inputs():
 
 # RoPE KAT constants (rope_cuda_test.cpp:210-220)
 ROPE_B, ROPE_S, ROPE_HQ, ROPE_HKV, ROPE_D, ROPE_P, ROPE_START, ROPE_THETA = 1, 3, 2, 1, 8, 16, 5, 1.0e6
+
+
+# KV cache KAT (kv_cache_cuda_test.cpp:124-138): 2 layers, batch 2, capacity 5, 2 KV heads of 4
+KV_LAYERS, KV_BATCH, KV_SEQ_CAP, KV_HEADS, KV_DIM = 2, 2, 5, 2, 4
+
+
+def kv_values(count, start):
+    """kv_cache_cuda_test.cpp:27-43: start + 0.25 i, rounded to bf16 to nearest even."""
+    bits = (np.float32(start) + np.arange(count, dtype=np.float32) * np.float32(0.25)).view(np.uint32).astype(np.uint64)
+    bits = bits + 0x7FFF + ((bits >> 16) & 1)
+    return (bits >> 16).astype(np.uint16)
+
+
+def kv_steps():
+    """(start, keys, values) of the test's prefill (2 tokens) and decode (1 token) appends, as [B, S, heads * dim]."""
+    P = KV_HEADS * KV_DIM
+    pre = (KV_BATCH, 2, P)
+    dec = (KV_BATCH, 1, P)
+    return [(0, kv_values(int(np.prod(pre)), 1.0).reshape(pre), kv_values(int(np.prod(pre)), 21.0).reshape(pre)),
+            (2, kv_values(int(np.prod(dec)), 41.0).reshape(dec), kv_values(int(np.prod(dec)), 61.0).reshape(dec))]

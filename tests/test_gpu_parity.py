@@ -366,3 +366,115 @@ def test_last_token_norm(q3k, hip, oracle, synth, B, S, H, add, offset):
         prim, lo, hi = oracle.rms_norm(last_h, w, EPS)
     check_exact(name + " residual (only last rows change)", h_got, expect_h)
     check_band(oracle, name, Y.get(np.uint16, (B, H)), prim, lo, hi)
+
+
+# ---------------------------------------------------------------- KV cache
+
+def test_kv_append_kat(q3k, hip, oracle):
+    """The reference test's prefill + decode appends into both layers (kv_cache_cuda_test.cpp:124-300)."""
+    announce("kv_append KAT")
+    L, Bc, Sc, P = kat.KV_LAYERS, kat.KV_BATCH, kat.KV_SEQ_CAP, kat.KV_HEADS * kat.KV_DIM
+    KC = Guarded(hip, np.zeros((L, Bc, Sc, P), np.uint16))
+    VC = Guarded(hip, np.zeros((L, Bc, Sc, P), np.uint16))
+    kc = np.zeros((L, Bc, Sc, P), np.uint16)
+    vc = np.zeros_like(kc)
+    layer_bytes = Bc * Sc * P * 2
+    for layer in range(L):
+        for start, k, v in kat.kv_steps():
+            K, V = Guarded(hip, k), Guarded(hip, v)
+            q3k.kv_append(K, V, KC.ptr + layer * layer_bytes, VC.ptr + layer * layer_bytes, k.shape[0], k.shape[1],
+                          P * 2, Sc, start)
+            kc[layer], vc[layer] = oracle.kv_append(k, v, kc[layer], vc[layer], start)
+    hip.synchronize()
+    assert KC.guards_intact() and VC.guards_intact()
+    check_exact("kv_append KAT keys", KC.get(np.uint16, kc.shape), kc)
+    check_exact("kv_append KAT values", VC.get(np.uint16, vc.shape), vc)
+
+
+@pytest.mark.parametrize("B,S,row,Bc,Sc,start,dtype,offset", [
+    (4, 33, 1024, 4, 64, 7, np.uint16, 0),     # Qwen3-8B KV row (8 heads x 128), prefill
+    (4, 1, 1024, 8, 64, 63, np.uint16, 0),     # decode into the last slot, batch below capacity
+    (2, 5, 1024, 2, 9, 4, np.float32, 0),      # fp32 cache
+    (3, 6, 3, 3, 10, 2, np.uint16, 0),         # 6-byte rows: 2-byte words
+    (2, 7, 1024, 2, 11, 1, np.uint16, 2),      # unaligned pointers: 2-byte words
+    (2, 4, 1024, 2, 4, 0, np.float32, 4),      # fp32, 4-byte aligned: 4-byte words
+    (1, 300, 256, 1, 300, 0, np.uint16, 0),    # full capacity in one append
+])
+def test_kv_append_shapes(q3k, hip, oracle, synth, B, S, row, Bc, Sc, start, dtype, offset):
+    name = f"kv_append B={B} S={S} row={row} cap=({Bc},{Sc}) start={start} {np.dtype(dtype).name} offset={offset}"
+    announce(name)
+    rng = np.random.default_rng(B * 1000 + S)
+    mk = (lambda shape: rng.standard_normal(shape).astype(np.float32)) if dtype == np.float32 else \
+        (lambda shape: rng.integers(0, 1 << 16, shape, dtype=np.uint16))
+    k, v = mk((B, S, row)), mk((B, S, row))
+    kc0, vc0 = mk((Bc, Sc, row)), mk((Bc, Sc, row))
+    K, V = Guarded(hip, k, offset=offset), Guarded(hip, v, offset=offset)
+    KC, VC = Guarded(hip, kc0, offset=offset), Guarded(hip, vc0, offset=offset)
+    q3k.kv_append(K, V, KC, VC, B, S, k[0, 0].nbytes, Sc, start)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (K, V, KC, VC))
+    kc, vc = oracle.kv_append(k, v, kc0, vc0, start)
+    view = np.uint32 if dtype == np.float32 else np.uint16
+    check_exact(name + " keys", KC.get(dtype, kc.shape).view(view), kc.view(view))
+    check_exact(name + " values", VC.get(dtype, vc.shape).view(view), vc.view(view))
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,D,Sc,cs,positions,offset", [
+    (2, 17, 32, 8, 128, 40, 5, None, 0),       # Qwen3-8B heads, prefill at cached length 5
+    (4, 1, 16, 8, 128, 64, 63, None, 0),       # decode step into the last slot
+    (3, 9, 8, 4, 128, 16, 0, "random", 0),     # per-token positions, one outside the table
+    (2, 12, 64, 4, 128, 12, 0, None, 0),       # Qwen3-32B shape, whole capacity
+    (2, 7, 4, 2, 64, 12, 3, None, 0),          # head_dim 64: generic path
+    (2, 5, 8, 4, 128, 8, 2, None, 2),          # unaligned: generic path
+])
+def test_qk_norm_rope_kv_append(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, Sc, cs, positions, offset):
+    """Fused Q/K norm + RoPE + KV append (self_attention.cpp:147-156) against the oracle composition, and bit for
+    bit against q3k_qk_norm_rope_bf16 followed by q3k_kv_append."""
+    name = f"qk_norm_rope_kv_append B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} cap={Sc} cs={cs} pos={positions} off={offset}"
+    announce(name)
+    P = 64
+    start = cs if positions is None else 0
+    q = synth.normal_bf16(130, Hq, (B, S, Hq * D))
+    k = synth.normal_bf16(131, Hkv, (B, S, Hkv * D))
+    v = synth.normal_bf16(132, Hkv, (B, S, Hkv * D))
+    qw = synth.normal_bf16(133, D, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(134, D, (D,), mean=1.0, std=0.1)
+    kc0 = synth.normal_bf16(135, Sc, (B + 1, Sc, Hkv * D))
+    vc0 = synth.normal_bf16(136, Sc, (B + 1, Sc, Hkv * D))
+    table = oracle.build_rope_cache(P, D, 1.0e6)
+    pos = None
+    if positions == "random":
+        pos = synth.uniform_positions(137, 1, B * S, P).reshape(B, S)
+        pos[1, 2] = P
+    Q, K, V = Guarded(hip, q, offset=offset), Guarded(hip, k, offset=offset), Guarded(hip, v, offset=offset)
+    QW, KW = Guarded(hip, qw, offset=offset), Guarded(hip, kw, offset=offset)
+    KC, VC = Guarded(hip, kc0, offset=offset), Guarded(hip, vc0, offset=offset)
+    C = Guarded(hip, table)
+    PZ = Guarded(hip, pos) if pos is not None else None
+    q3k.qk_norm_rope_kv_append(Q, K, V, QW, KW, B, S, Hq, Hkv, D, EPS, C, P, start, KC, VC, Sc, cs, PZ)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (Q, K, V, QW, KW, KC, VC, C))
+    check_exact(name + " k input unchanged", K.get(np.uint16, k.shape), k)
+    check_exact(name + " v input unchanged", V.get(np.uint16, v.shape), v)
+    got_q = Q.get(np.uint16, q.shape)
+    got_kc, got_vc = KC.get(np.uint16, kc0.shape), VC.get(np.uint16, vc0.shape)
+
+    prim_q, lo_q, hi_q = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, table, start, pos)
+    check_band(oracle, name + " q", got_q, prim_q, lo_q, hi_q)
+    prim_k, lo_k, hi_k = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, table, start, pos)
+    rows = (slice(0, B), slice(cs, cs + S))
+    check_band(oracle, name + " k cache rows", got_kc[rows], prim_k, lo_k, hi_k)
+    exp_kc, exp_vc = oracle.kv_append(prim_k, v, kc0, vc0, cs)
+    untouched = np.ones(kc0.shape, bool)
+    untouched[rows] = False
+    check_exact(name + " k cache elsewhere untouched", got_kc[untouched], kc0[untouched])
+    check_exact(name + " v cache", got_vc, exp_vc)
+
+    # bit-identity with the two-step drop-in path
+    Q2, K2 = Guarded(hip, q, offset=offset), Guarded(hip, k, offset=offset)
+    KC2, VC2 = Guarded(hip, kc0, offset=offset), Guarded(hip, vc0, offset=offset)
+    q3k.qk_norm_rope(Q2, K2, QW, KW, B, S, Hq, Hkv, D, EPS, C, P, start, PZ)
+    q3k.kv_append(K2, V, KC2, VC2, B, S, Hkv * D * 2, Sc, cs)
+    hip.synchronize()
+    check_exact(name + " q == qk_norm_rope", got_q, Q2.get(np.uint16, q.shape))
+    check_exact(name + " k cache == qk_norm_rope + kv_append", got_kc, KC2.get(np.uint16, kc0.shape))

@@ -345,3 +345,45 @@ def test_qk_norm_rope_is_composition(oracle, synth):
     pos = np.tile(3 + np.arange(S), B)
     ref = hf_rope(normed_t, heads, D, cache, pos).reshape(x.shape)
     assert_matches_where_unambiguous(fused, lo, hi, ref, "qk_norm_rope", min_exact=0.99)
+
+
+# ---------------------------------------------------------------- KV cache
+
+def test_kv_append_kat(oracle):
+    """The reference test's scenario (kv_cache_cuda_test.cpp:124-300): prefill of 2 tokens and a decode step into
+    both layers; every slot checked with the test's own index formula (verify_slice, :61-113), the rest stays 0."""
+    L, Bc, Sc, P = kat.KV_LAYERS, kat.KV_BATCH, kat.KV_SEQ_CAP, kat.KV_HEADS * kat.KV_DIM
+    kc = np.zeros((L, Bc, Sc, P), np.uint16)
+    vc = np.zeros_like(kc)
+    steps = kat.kv_steps()
+    for layer in range(L):
+        for start, k, v in steps:
+            kc[layer], vc[layer] = oracle.kv_append(k, v, kc[layer], vc[layer], start)
+    flat_k, flat_v = kc.reshape(-1), vc.reshape(-1)
+    written = np.zeros(flat_k.size, bool)
+    for layer in range(L):
+        for start, k, v in steps:
+            S = k.shape[1]
+            for b in range(Bc):
+                for t in range(S):
+                    for col in range(P):
+                        dst = ((layer * Bc + b) * Sc + start + t) * P + col
+                        src = (b * S + t) * P + col
+                        assert flat_k[dst] == k.reshape(-1)[src] and flat_v[dst] == v.reshape(-1)[src]
+                        written[dst] = True
+    assert not flat_k[~written].any() and not flat_v[~written].any()
+    # the decode values of the test include one that bf16 must round: 61 + 0.25 * 15 = 64.75 -> 64.5 or 65
+    assert kat.kv_values(16, 61.0)[15] == oracle.bf16(64.75)
+
+
+def test_kv_append_fp32_rows_and_bytes(oracle, synth):
+    """Bytes are copied unchanged whatever the element type (the reference cache also takes Float32)."""
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((3, 4, 24)).astype(np.float32)
+    v = rng.standard_normal((3, 4, 24)).astype(np.float32)
+    kc = np.full((4, 9, 24), np.nan, np.float32)
+    vc = np.full((4, 9, 24), np.nan, np.float32)
+    kc2, vc2 = oracle.kv_append(k, v, kc, vc, 5)
+    assert np.array_equal(kc2[:3, 5:9].view(np.uint32), k.view(np.uint32))
+    assert np.array_equal(vc2[:3, 5:9].view(np.uint32), v.view(np.uint32))
+    assert np.isnan(kc2[3]).all() and np.isnan(kc2[:, :5]).all() and np.isnan(vc2[:, :5]).all()
