@@ -169,6 +169,25 @@ Q3K_API int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k,
                           const int32_t *positions, q3k_stream_t stream);
 
 /*
+ * Causal grouped-query attention.  q [B, S, Hq * D] bf16 (contiguous);
+ * k_cache / v_cache are [B, cached, Hkv, D] bf16 views given by element
+ * strides k_strides[4] / v_strides[4] (batch, position, head, dim), e.g. a
+ * KV cache layer with strides {Smax * Hkv * D, Hkv * D, D, 1}.  Query
+ * (b, s) attends to keys 0 .. start + s; query head h reads KV head
+ * h / (Hq / Hkv); scale 1 / sqrt(D).  cached must equal start + S.
+ * out [B, S, Hq * D] bf16.  head_dim 128 with unit dim stride and 16-byte
+ * aligned rows takes the matrix-core kernel, anything up to 256 the generic
+ * one.  Replaces qwen3::ops::grouped_query_attention,
+ * src/ops/gqa_attention.cu:304-345 (kernel :20-155, checks :157-302).
+ */
+Q3K_API int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache,
+                          const uint16_t *v_cache, uint16_t *out, int64_t B,
+                          int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
+                          int64_t cached, int64_t start,
+                          const int64_t *k_strides, const int64_t *v_strides,
+                          q3k_stream_t stream);
+
+/*
  * KV-cache append: K and V [B, S, row_bytes] (contiguous) are copied to rows
  * start .. start + S - 1 of batch rows 0 .. B - 1 of one layer's cache
  * [batch_cap, seq_cap, row_bytes] (key_cache / value_cache point at the

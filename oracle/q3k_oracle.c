@@ -539,3 +539,178 @@ void q3o_kv_append(const void *k, const void *v, void *kc, void *vc, int64_t B, 
         memcpy((char *)vc + b * dst_pitch + start * row_bytes, (const char *)v + b * width, (size_t)width);
     }
 }
+
+/* ---- grouped-query attention: src/ops/gqa_attention.cu:20-155 ------------ */
+
+struct attn_ctx
+{
+    const uint16_t *q, *k, *v;
+    int64_t S;
+    int32_t Hq, Hkv, D;
+    int64_t cached, start;
+    const int64_t *ks, *vs;
+    const int64_t *rows;
+    uint16_t *out, *lo, *hi;
+    float scale;
+};
+
+/* The kernel's dot product: thread t < D holds q_t * k_t, threads D..255
+ * hold 0, then the shared-memory tree with offsets 128, 64, ..., 1
+ * (gqa_attention.cu:75-104). */
+static float attn_ref_dot(const float *qv, const uint16_t *kp, int64_t kd, int D)
+{
+    float r[256];
+    for (int t = 0; t < 256; ++t)
+        r[t] = t < D ? qv[t] * FB(kp[t * kd]) : 0.0f;
+    for (int off = 128; off > 0; off /= 2)
+        for (int t = 0; t < off; ++t)
+            r[t] += r[t + off];
+    return r[0];
+}
+
+/* Half-width of the band on one output: a first-order bound on what fp32
+ * arithmetic can change, relative to the value in double.  Terms: the dot
+ * product, summed by the reference as a binary tree of depth 8 (256 slots)
+ * and by a matrix-core kernel in at most 16 rounded steps (chunks of exact
+ * products), hence gamma_16 on sum |q k| (a sum of depth d errs by at most
+ * gamma_d sum |x|); the
+ * scale product, the subtraction and exp of each weight (4 u for expf, 2 u on
+ * the argument), one exp-and-multiply per later rescale of the running
+ * maximum, and the accumulation of numerator and denominator over the visible
+ * keys, bounded probabilistically (Higham and Mary, SIAM J. Sci. Comput. 41
+ * (2019) A2815: lambda * sqrt(n) * u with lambda = 8, failing with probability
+ * below 2 n exp(-32) per output) because a worst-case
+ * n * u for n in the thousands would exceed a bf16 ulp without any
+ * implementation coming near it.  The divide adds 2 u. */
+static void attn_band(const struct attn_ctx *c, const float *qv, const uint16_t *kb, const uint16_t *vb,
+                      int64_t vis, double *work, const float *prim, uint16_t *lo, uint16_t *hi)
+{
+    const double u = ldexp(1.0, -24);
+    const int D = c->D;
+    const double gD = 16.0 * u / (1.0 - 16.0 * u);
+    const double gL = 8.0 * sqrt(3.0 * (double)vis) * u;
+    const double e_exp = 4.0 * u;
+    double *sd = work, *ad = work + vis, *rj = work + 2 * vis;
+    double M = -INFINITY;
+    for (int64_t j = 0; j < vis; ++j)
+    {
+        const uint16_t *kp = kb + j * c->ks[1];
+        double s = 0.0, a = 0.0;
+        for (int t = 0; t < D; ++t)
+        {
+            const double p = (double)qv[t] * (double)FB(kp[t * c->ks[3]]);
+            s += p;
+            a += fabs(p);
+        }
+        sd[j] = s * (double)c->scale;
+        ad[j] = a * (double)c->scale;
+        if (sd[j] > M)
+            M = sd[j];
+    }
+    /* rescales after key j: strict increases of the running maximum */
+    double run = -INFINITY, later = 0.0;
+    for (int64_t j = 0; j < vis; ++j)
+    {
+        rj[j] = (j > 0 && sd[j] > run) ? 1.0 : 0.0;
+        if (sd[j] > run)
+            run = sd[j];
+    }
+    for (int64_t j = vis - 1; j >= 0; --j)
+    {
+        const double inc = rj[j];
+        rj[j] = later + 1.0;
+        later += inc;
+    }
+    double den = 0.0, eden = 0.0;
+    for (int64_t j = 0; j < vis; ++j)
+    {
+        const double w = exp(sd[j] - M);
+        const double e = gD * ad[j] + u * fabs(sd[j]) + 2.0 * u * fabs(sd[j] - M) + e_exp + rj[j] * (e_exp + 2.0 * u);
+        den += w;
+        eden += w * e;
+        sd[j] = w; /* reuse: weight */
+        ad[j] = e; /* reuse: relative error of the weight */
+    }
+    eden += gL * den;
+    for (int t = 0; t < D; ++t)
+    {
+        double num = 0.0, absn = 0.0, enum_ = 0.0;
+        for (int64_t j = 0; j < vis; ++j)
+        {
+            const double x = (double)FB(vb[j * c->vs[1] + t * c->vs[3]]);
+            num += sd[j] * x;
+            absn += sd[j] * fabs(x);
+            enum_ += sd[j] * fabs(x) * ad[j];
+        }
+        enum_ += gL * absn;
+        const double o = num / den;
+        const double E = (enum_ + fabs(o) * eden) / den + 2.0 * u * fabs(o);
+        const uint16_t p = BF(prim[t]);
+        lo[t] = min_bf(bf_of_double(o - E), p);
+        hi[t] = max_bf(bf_of_double(o + E), p);
+    }
+}
+
+static void attn_range(void *p, int64_t b, int64_t e)
+{
+    const struct attn_ctx *c = (const struct attn_ctx *)p;
+    const int D = c->D;
+    const int32_t G = c->Hq / c->Hkv;
+    double *work = (double *)malloc(sizeof(double) * 3 * (size_t)(c->cached > 0 ? c->cached : 1));
+    float qv[256], acc[256], res[256];
+    for (int64_t i = b; i < e; ++i)
+    {
+        const int64_t row = c->rows ? c->rows[i] : i;
+        const int32_t h = (int32_t)(row % c->Hq);
+        const int64_t bs = row / c->Hq;
+        const int64_t s = bs % c->S, bi = bs / c->S;
+        const int32_t kvh = h / G;
+        const int64_t vis = c->start + s + 1;
+        const uint16_t *kb = c->k + bi * c->ks[0] + kvh * c->ks[2];
+        const uint16_t *vb = c->v + bi * c->vs[0] + kvh * c->vs[2];
+        for (int t = 0; t < D; ++t)
+        {
+            qv[t] = FB(c->q[row * D + t]);
+            acc[t] = 0.0f;
+        }
+        float m = -INFINITY, l = 0.0f;
+        for (int64_t j = 0; j < vis; ++j)
+        {
+            const float score = attn_ref_dot(qv, kb + j * c->ks[1], c->ks[3], D) * c->scale;
+            const float nm = fmaxf(m, score);
+            const float ow = (float)exp((double)(m - nm)); /* stands in for expf (:111) */
+            const float nw = (float)exp((double)(score - nm));
+            l = fmaf(l, ow, nw);
+            const uint16_t *vp = vb + j * c->vs[1];
+            for (int t = 0; t < D; ++t)
+                acc[t] = fmaf(FB(vp[t * c->vs[3]]), nw, acc[t] * ow);
+            m = nm;
+        }
+        for (int t = 0; t < D; ++t)
+        {
+            res[t] = acc[t] / l;
+            c->out[i * D + t] = BF(res[t]);
+        }
+        if (c->lo && c->hi)
+            attn_band(c, qv, kb, vb, vis, work, res, c->lo + i * D, c->hi + i * D);
+    }
+    free(work);
+}
+
+int q3o_gqa_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, int64_t B, int64_t S, int32_t Hq,
+                      int32_t Hkv, int32_t D, int64_t cached, int64_t start, const int64_t *k_strides,
+                      const int64_t *v_strides, const int64_t *rows, int64_t nrows, uint16_t *out, uint16_t *lo,
+                      uint16_t *hi, int nthreads)
+{
+    if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D <= 0 || D > 256 || start < 0 ||
+        start + S != cached)
+        return -1;
+    const int64_t total = B * S * Hq;
+    for (int64_t i = 0; rows && i < nrows; ++i)
+        if (rows[i] < 0 || rows[i] >= total)
+            return -1;
+    struct attn_ctx c = {q, k, v, S, Hq, Hkv, D, cached, start, k_strides, v_strides, rows, out, lo, hi,
+                         1.0f / sqrtf((float)D)}; /* host scale, gqa_attention.cu:322 */
+    parallel_for(rows ? nrows : total, nthreads, attn_range, &c);
+    return 0;
+}

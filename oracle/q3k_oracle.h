@@ -78,6 +78,19 @@ int q3o_qk_norm_rope(uint16_t *x, const uint16_t *w, int64_t B, int64_t S, int32
 void q3o_kv_append(const void *k, const void *v, void *kc, void *vc, int64_t B, int64_t S, int64_t row_bytes,
                    int64_t seq_cap, int64_t start);
 
+/* Grouped-query attention, src/ops/gqa_attention.cu:20-155 and :304-345:
+ * query [B, S, Hq * D]; key/value caches addressed as
+ * k[b * ks[0] + j * ks[1] + h * ks[2] + d * ks[3]] (element strides of the
+ * [B, cached, Hkv, D] views); query (b, s) sees keys 0 .. start + s, which
+ * requires cached == start + S.  Primary: the kernel's order (256-slot tree
+ * dot, online softmax with fmaf updates, final divide).  rows (optional)
+ * lists row indices (b * S + s) * Hq + h to compute; out/lo/hi hold
+ * [nrows or B * S * Hq, D].  Returns 0, or -1 on bad arguments. */
+int q3o_gqa_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, int64_t B, int64_t S, int32_t Hq,
+                      int32_t Hkv, int32_t D, int64_t cached, int64_t start, const int64_t *k_strides,
+                      const int64_t *v_strides, const int64_t *rows, int64_t nrows, uint16_t *out, uint16_t *lo,
+                      uint16_t *hi, int nthreads);
+
 /* Comparison of kernel output against (primary, lo, hi).
  * stats[0] = elements, [1] = failures (outside [lo-1, hi+1]),
  * [2] = first failing index or -1, [3] = ambiguous elements (lo != hi),

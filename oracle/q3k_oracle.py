@@ -35,6 +35,8 @@ def lib() -> ctypes.CDLL:
             "q3o_rope": ([_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p, _p, _int], _int),
             "q3o_qk_norm_rope": ([_p, _p, _i64, _i64, _i32, _i32, _f32, _p, _i64, _i64, _p, _p, _p, _int], _int),
             "q3o_kv_append": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64], None),
+            "q3o_gqa_attention": ([_p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p,
+                                   _int], _int),
             "q3o_compare_band": ([_p, _p, _p, _p, _i64, _p], None),
             "q3o_ulp_distance": ([ctypes.c_uint16, ctypes.c_uint16], ctypes.c_int32),
             "q3o_bf16_from_f32": ([_f32], ctypes.c_uint16),
@@ -159,6 +161,30 @@ def kv_append(k, v, k_cache, v_cache, start):
     seq_cap = kc.shape[1]
     lib().q3o_kv_append(_ptr(k), _ptr(v), _ptr(kc), _ptr(vc), B, S, row_bytes, seq_cap, start)
     return kc, vc
+
+
+def gqa_attention(q, k_cache, v_cache, Hq, start, rows=None, band=True, nthreads=None):
+    """q [B, S, Hq * D] bf16; k_cache / v_cache [B, cached, Hkv, D] bf16 (any strides, e.g. views of a larger
+    cache).  Returns (out, lo, hi) shaped [B, S, Hq * D], or [len(rows), D] when rows is given."""
+    q = _a(q, np.uint16)
+    B, S = q.shape[0], q.shape[1]
+    _, cached, Hkv, D = k_cache.shape
+    assert k_cache.dtype == np.uint16 and v_cache.dtype == np.uint16 and v_cache.shape == k_cache.shape
+    ks = np.array([st // 2 for st in k_cache.strides], np.int64)
+    vs = np.array([st // 2 for st in v_cache.strides], np.int64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    n = B * S * Hq if r is None else r.size
+    out = np.empty((n, D), np.uint16)
+    lo, hi = _bands((n, D), band)
+    st = lib().q3o_gqa_attention(_ptr(q), k_cache.ctypes.data, v_cache.ctypes.data, B, S, Hq, Hkv, D, cached, start,
+                                 _ptr(ks), _ptr(vs), _ptr(r), n, _ptr(out), _ptr(lo), _ptr(hi),
+                                 nthreads or default_threads())
+    if st != 0:
+        raise ValueError("bad attention arguments")
+    if r is None:
+        shape = (B, S, Hq * D)
+        return out.reshape(shape), None if lo is None else lo.reshape(shape), None if hi is None else hi.reshape(shape)
+    return out, lo, hi
 
 
 def compare(got, primary, lo=None, hi=None) -> dict:

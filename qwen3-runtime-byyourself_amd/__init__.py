@@ -80,6 +80,7 @@ SIGNATURES = {
     "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
+    "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p],
     "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "q3k_qk_norm_rope_kv_append_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p,
                                         _p, _p, _i64, _i64, _p],
@@ -181,6 +182,14 @@ def rope(x, B, S, heads, D, cache, P, start, positions=None, stream=None):
 def qk_norm_rope(q, k, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, positions=None, stream=None):
     _check(load().q3k_qk_norm_rope_bf16(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw), B, S, Hq, Hkv, D, eps,
                                         _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
+
+
+def gqa_attention(q, k_cache, v_cache, out, B, S, Hq, Hkv, D, cached, start, k_strides, v_strides, stream=None):
+    """k_strides / v_strides: 4 element strides (batch, position, head, dim) of the cache views."""
+    ks = (ctypes.c_int64 * 4)(*[int(x) for x in k_strides])
+    vs = (ctypes.c_int64 * 4)(*[int(x) for x in v_strides])
+    _check(load().q3k_gqa_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), B, S, Hq, Hkv, D, cached,
+                                         start, ctypes.cast(ks, _p), ctypes.cast(vs, _p), _ptr(stream)))
 
 
 def kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, start, stream=None):

@@ -1,0 +1,412 @@
+// Causal grouped-query attention for gfx950 (src/ops/gqa_attention.cu:20-155
+// of the reference: query [B, S, Hq * D], key/value cache views
+// [B, cached, Hkv, D] with strides, query (b, s) attends to keys
+// 0 .. start + s, query head h reads KV head h / (Hq / Hkv)).
+//
+// Matrix-core path (head_dim 128, unit dim stride, 16-byte rows): a block of
+// four waves owns one (batch, KV head) and QP query positions of all G heads
+// of that group, so every K/V tile it stages in LDS serves G heads.  A wave's
+// 32 "columns" are (position, head) pairs.  Per tile of 32 keys:
+//   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16: A = K rows from LDS,
+//                 B = the wave's Q fragments (registers for the whole loop);
+//   online softmax per column: a lane holds one column, so the key max and
+//                 sum need only its 16 registers and the lane 32 apart;
+//   O^T += V^T P^T: A = V^T from a transposed LDS copy of the tile, B = P^T
+//                 straight from the S^T registers.  P is split into a bf16
+//                 high part and a bf16 remainder (two MFMAs), so the weights
+//                 keep about 16 significant bits: the reference accumulates
+//                 p * v in fp32, and a single bf16 rounding of p would cost
+//                 up to half an output ulp.
+// Scores are scaled by scale * log2(e) and exponentiated with v_exp_f32.
+// The next tile's K and V are loaded into registers while the current one
+// is computed.
+//
+// Generic path (any head_dim <= 256, any strides): one wave per query row,
+// keys in order, lanes over the head dimension -- the reference's own
+// structure with wave reductions.
+#include "q3k_common.hpp"
+
+namespace q3k
+{
+    namespace
+    {
+        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+        typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+        constexpr int kAttD = 128;
+        constexpr int kKeyTile = 32;
+        constexpr int kKRowBytes = kAttD * 2 + 16;   // K tile row in LDS, padded: conflict-free b128 reads
+        constexpr int kVtRowBytes = kKeyTile * 2 + 16; // V^T tile row (one head-dim index), padded likewise
+        constexpr int kKTileBytes = kKeyTile * kKRowBytes;
+        constexpr int kVtTileBytes = kAttD * kVtRowBytes;
+        constexpr float kLog2e = 1.4426950408889634f;
+
+        struct AttnArgs
+        {
+            const uint16_t *q;
+            const uint16_t *k;
+            const uint16_t *v;
+            uint16_t *out;
+            int64_t S;
+            int64_t start;
+            int64_t ks0, ks1, ks2, ks3;
+            int64_t vs0, vs1, vs2, vs3;
+            int32_t Hq;
+            int32_t Hkv;
+            int32_t D;
+            int32_t qblocks;
+            float scale;
+        };
+
+        __device__ __forceinline__ bf16x8_t as_bf8(const Vec8 &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+        // LDS position of key kk (0..31) in a V^T row: bits 2 and 3 swapped, so
+        // that the 8 keys lane group g feeds to the PV MFMA of chunk m (keys
+        // 16m + 8h + 4g + j, h < 2, j < 4: the S^T accumulator rows the lane
+        // holds) are 8 consecutive positions 16m + 8g .. + 7.
+        __device__ __forceinline__ int vt_pos(int kk) { return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1); }
+
+        __device__ __forceinline__ uint32_t bf_pair(uint32_t lo_word, uint32_t hi_word, int half)
+        {
+            // element `half` (0 = low) of each word, low word's element in the low half
+            return half == 0 ? ((lo_word & 0xffffu) | (hi_word << 16)) : ((lo_word >> 16) | (hi_word & 0xffff0000u));
+        }
+
+        template <int G>
+        __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a)
+        {
+            constexpr int PW = 32 / G; // query positions per wave
+            constexpr int QP = 4 * PW; // per block
+            __shared__ __attribute__((aligned(16))) unsigned char lds[kKTileBytes + kVtTileBytes];
+            unsigned char *k_lds = lds;
+            unsigned char *vt_lds = lds + kKTileBytes;
+
+            const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+            const int lane = threadIdx.x % kWave;
+            const int li = lane % 32, lg = lane / 32;
+
+            // block -> (batch, KV head, query block); the longest query blocks go first
+            int bid = blockIdx.x;
+            const int qb = a.qblocks - 1 - bid % a.qblocks;
+            bid /= a.qblocks;
+            const int kvh = bid % a.Hkv;
+            const int64_t b = bid / a.Hkv;
+            const int64_t s0 = static_cast<int64_t>(qb) * QP;
+            const int64_t s_last = (s0 + QP < a.S ? s0 + QP : a.S) - 1;
+            const int64_t n_keys = a.start + s_last + 1;
+            const int ntiles = static_cast<int>((n_keys + kKeyTile - 1) / kKeyTile);
+
+            // this lane's column
+            const int64_t wave_s0 = s0 + wave * PW;
+            const int64_t s_col = wave_s0 + li / G;
+            const int h_col = kvh * G + li % G;
+            const bool col_ok = s_col < a.S;
+            const int64_t last_key = a.start + s_col;
+            const bool wave_active = wave_s0 < a.S;
+            const bool wave_partial = wave_s0 + PW > a.S;
+
+            bf16x8_t qf[kAttD / 16];
+            {
+                const Vec8 *qrow = reinterpret_cast<const Vec8 *>(a.q + ((b * a.S + s_col) * a.Hq + h_col) * kAttD);
+                const Vec8 zero = {{0u, 0u, 0u, 0u}};
+#pragma unroll
+                for (int c = 0; c < kAttD / 16; ++c)
+                    qf[c] = as_bf8(col_ok ? qrow[2 * c + lg] : zero);
+            }
+
+            const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;
+            const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;
+            // staging: K chunks (key = id / 16, 16-byte chunk id % 16 of the row), V key pair x 8 dims
+            const int k_key0 = threadIdx.x / 16, k_chunk = threadIdx.x % 16;
+            const int v_chunk = threadIdx.x / 16, v_pair = threadIdx.x % 16;
+            Vec8 kst[2], vst[2];
+            auto load_tile = [&](int tile) {
+                const int64_t key0 = static_cast<int64_t>(tile) * kKeyTile;
+                const Vec8 zero = {{0u, 0u, 0u, 0u}};
+#pragma unroll
+                for (int x = 0; x < 2; ++x)
+                {
+                    const int64_t key = key0 + k_key0 + 16 * x;
+                    kst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(kbase + key * a.ks1) + k_chunk)
+                                          : zero;
+                }
+#pragma unroll
+                for (int x = 0; x < 2; ++x)
+                {
+                    const int64_t key = key0 + 2 * v_pair + x;
+                    vst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(vbase + key * a.vs1) + v_chunk)
+                                          : zero;
+                }
+            };
+            auto store_tile = [&]() {
+#pragma unroll
+                for (int x = 0; x < 2; ++x)
+                    *reinterpret_cast<Vec8 *>(k_lds + (k_key0 + 16 * x) * kKRowBytes + k_chunk * 16) = kst[x];
+                const int pos = vt_pos(2 * v_pair);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                {
+                    const uint32_t w = bf_pair(vst[0].d[e / 2], vst[1].d[e / 2], e % 2);
+                    *reinterpret_cast<uint32_t *>(vt_lds + (8 * v_chunk + e) * kVtRowBytes + pos * 2) = w;
+                }
+            };
+
+            f32x16_t o[kAttD / 32];
+#pragma unroll
+            for (int dt = 0; dt < kAttD / 32; ++dt)
+                o[dt] = f32x16_t{};
+            float m = -__builtin_huge_valf(), l = 0.0f;
+            const float scale2 = a.scale * kLog2e;
+
+            load_tile(0);
+            for (int tile = 0; tile < ntiles; ++tile)
+            {
+                __syncthreads(); // the previous tile has been consumed
+                store_tile();
+                __syncthreads();
+                if (tile + 1 < ntiles)
+                    load_tile(tile + 1);
+                if (!wave_active)
+                    continue;
+                const int64_t key0 = static_cast<int64_t>(tile) * kKeyTile;
+
+                f32x16_t sacc = f32x16_t{};
+#pragma unroll
+                for (int c = 0; c < kAttD / 16; ++c)
+                {
+                    const Vec8 kf = *reinterpret_cast<const Vec8 *>(k_lds + li * kKRowBytes + (16 * c + 8 * lg) * 2);
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kf), qf[c], sacc, 0, 0, 0);
+                }
+
+                const bool need_mask = key0 + kKeyTile - 1 > a.start + wave_s0 || wave_partial;
+                float sc[16];
+                float mloc = -__builtin_huge_valf();
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    float x = sacc[r] * scale2;
+                    if (need_mask)
+                    {
+                        const int64_t kk = key0 + 8 * (r / 4) + 4 * lg + (r % 4);
+                        if (kk > last_key || !col_ok)
+                            x = -__builtin_huge_valf();
+                    }
+                    sc[r] = x;
+                    mloc = fmaxf(mloc, x);
+                }
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+                const float m_new = fmaxf(m, mloc);
+                const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+                float p[16];
+                float psum = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    p[r] = __builtin_amdgcn_exp2f(sc[r] - m_use);
+                    psum += p[r];
+                }
+                psum += __shfl_xor(psum, 32);
+                l = l * alpha + psum;
+                m = m_new;
+#pragma unroll
+                for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        o[dt][r] *= alpha;
+
+                bf16x8_t phi[2], plo[2];
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm)
+                {
+                    Vec8 h8, l8;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        const float x0 = p[8 * mm + 2 * j], x1 = p[8 * mm + 2 * j + 1];
+                        const uint32_t hp = pack_rne(x0, x1);
+                        h8.d[j] = hp;
+                        l8.d[j] = pack_rne(x0 - bf_lo(hp), x1 - bf_hi(hp));
+                    }
+                    phi[mm] = as_bf8(h8);
+                    plo[mm] = as_bf8(l8);
+                }
+#pragma unroll
+                for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                    for (int mm = 0; mm < 2; ++mm)
+                    {
+                        const Vec8 vf = *reinterpret_cast<const Vec8 *>(vt_lds + (dt * 32 + li) * kVtRowBytes +
+                                                                         (16 * mm + 8 * lg) * 2);
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), phi[mm], o[dt], 0, 0, 0);
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), plo[mm], o[dt], 0, 0, 0);
+                    }
+            }
+
+            if (!col_ok)
+                return;
+            const float inv = 1.0f / l;
+            uint16_t *orow = a.out + ((b * a.S + s_col) * a.Hq + h_col) * kAttD;
+#pragma unroll
+            for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                {
+                    const int d = dt * 32 + 8 * q4 + 4 * lg;
+                    uint2 w;
+                    w.x = pack_rne(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv);
+                    w.y = pack_rne(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+                    *reinterpret_cast<uint2 *>(orow + d) = w;
+                }
+        }
+
+        // Generic path: one wave per query row (b, s, h); lane t holds head
+        // dims t, t + 64, ... (head_dim <= 256); keys in order with the online
+        // softmax of the reference.
+        __global__ __launch_bounds__(kBlock) void attn_generic_kernel(AttnArgs a, int64_t rows)
+        {
+            const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
+                                __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+            if (row >= rows)
+                return;
+            const int lane = threadIdx.x % kWave;
+            const int h = static_cast<int>(row % a.Hq);
+            const int64_t bs = row / a.Hq;
+            const int64_t s = bs % a.S, b = bs / a.S;
+            const int kvh = h / (a.Hq / a.Hkv);
+            const int D = a.D;
+            float qv[4], acc[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+            {
+                const int d = lane + 64 * x;
+                qv[x] = d < D ? bf_to_f(a.q[row * D + d]) : 0.0f;
+                acc[x] = 0.0f;
+            }
+            const uint16_t *kb = a.k + b * a.ks0 + kvh * a.ks2;
+            const uint16_t *vb = a.v + b * a.vs0 + kvh * a.vs2;
+            float m = -__builtin_huge_valf(), l = 0.0f;
+            const int64_t vis = a.start + s + 1;
+            for (int64_t j = 0; j < vis; ++j)
+            {
+                float part = 0.0f;
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                {
+                    const int d = lane + 64 * x;
+                    if (d < D)
+                        part = __builtin_fmaf(qv[x], bf_to_f(kb[j * a.ks1 + d * a.ks3]), part);
+                }
+                const float score = group_sum<64>(part) * a.scale;
+                const float nm = fmaxf(m, score);
+                const float ow = __expf(m - nm);
+                const float nw = __expf(score - nm);
+                l = __builtin_fmaf(l, ow, nw);
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                {
+                    const int d = lane + 64 * x;
+                    if (d < D)
+                        acc[x] = __builtin_fmaf(bf_to_f(vb[j * a.vs1 + d * a.vs3]), nw, acc[x] * ow);
+                }
+                m = nm;
+            }
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+            {
+                const int d = lane + 64 * x;
+                if (d < D)
+                    a.out[row * D + d] = f_to_bf(acc[x] / l);
+            }
+        }
+
+        bool mfma_ok(const AttnArgs &a, int32_t G)
+        {
+            const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32;
+            return g_ok && a.D == kAttD && a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
+                   a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 && aligned16(a.q) &&
+                   aligned16(a.k) && aligned16(a.v) && aligned_to(a.out, 8);
+        }
+
+        template <int G>
+        void launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
+        {
+            constexpr int QP = 4 * (32 / G);
+            a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
+            const int64_t blocks = B * a.Hkv * a.qblocks;
+            attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(a);
+        }
+    } // namespace
+} // namespace q3k
+
+extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                      uint16_t *out, int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
+                                      int64_t cached, int64_t start, const int64_t *k_strides,
+                                      const int64_t *v_strides, q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (B < 0 || S < 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA batch and sequence sizes cannot be negative");
+    if (Hq <= 0 || Hkv <= 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA head counts must be positive");
+    if (Hq % Hkv != 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA query heads must be divisible by key/value heads");
+    if (D <= 0 || D > 256)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA head_dim must be between 1 and 256");
+    if (start < 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA start_position cannot be negative");
+    if (start > cached || S != cached - start)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA cache length must equal start_position + sequence_length");
+    if (B == 0 || S == 0)
+        return Q3K_OK;
+    if (k_strides == nullptr || v_strides == nullptr)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA stride arrays are null");
+    for (int i = 0; i < 4; ++i)
+        if (k_strides[i] < 0 || v_strides[i] < 0)
+            return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA cache strides cannot be negative");
+    if (q == nullptr || k_cache == nullptr || v_cache == nullptr || out == nullptr)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA received a null pointer");
+    if (!aligned_to(q, 2) || !aligned_to(k_cache, 2) || !aligned_to(v_cache, 2) || !aligned_to(out, 2))
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "GQA pointers must be 2-byte aligned");
+    if (S > INT64_MAX / B || B * S > INT64_MAX / Hq || B * S * Hq > INT32_MAX)
+        return set_error(Q3K_ERR_OVERFLOW, "GQA grid is too large");
+
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    AttnArgs a{q,
+               k_cache,
+               v_cache,
+               out,
+               S,
+               start,
+               k_strides[0],
+               k_strides[1],
+               k_strides[2],
+               k_strides[3],
+               v_strides[0],
+               v_strides[1],
+               v_strides[2],
+               v_strides[3],
+               Hq,
+               Hkv,
+               D,
+               0,
+               1.0f / __builtin_sqrtf(static_cast<float>(D))};
+    const int32_t G = Hq / Hkv;
+    if (mfma_ok(a, G))
+    {
+        switch (G)
+        {
+        case 1: launch_mfma<1>(a, B, s); break;
+        case 2: launch_mfma<2>(a, B, s); break;
+        case 4: launch_mfma<4>(a, B, s); break;
+        case 8: launch_mfma<8>(a, B, s); break;
+        case 16: launch_mfma<16>(a, B, s); break;
+        default: launch_mfma<32>(a, B, s); break;
+        }
+        return check_launch("grouped_query_attention");
+    }
+    const int64_t rows = B * S * Hq;
+    const int64_t blocks = (rows + (kBlock / kWave) - 1) / (kBlock / kWave);
+    attn_generic_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(a, rows);
+    return check_launch("grouped_query_attention (generic)");
+}

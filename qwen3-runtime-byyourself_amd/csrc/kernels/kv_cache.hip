@@ -107,6 +107,8 @@ extern "C" int q3k_kv_append(const void *key, const void *value, void *key_cache
     using namespace q3k;
     if (const int st = validate_kv_append(key, value, key_cache, value_cache, B, S, row_bytes, seq_cap, start))
         return st;
+    if (B == 0 || S == 0)
+        return Q3K_OK;
     launch_kv_append(key, value, key_cache, value_cache, B, S, row_bytes, seq_cap, start,
                      reinterpret_cast<hipStream_t>(stream));
     return check_launch("kv_cache_append");

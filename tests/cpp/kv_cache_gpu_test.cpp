@@ -5,10 +5,12 @@
 // against the reference's op sequence bit for bit.
 #include "gpu_util.hpp"
 #include "qwen3/model/kv_cache.h"
+#include "qwen3/ops/gqa_attention.h"
 #include "qwen3/ops/kv_append.h"
 #include "qwen3/ops/rms_norm.h"
 #include "qwen3/ops/rope.h"
 
+#include <cmath>
 #include <cstring>
 
 using qwen3::DType;
@@ -154,6 +156,51 @@ namespace
             "RoPE range past the table accepted");
     }
 
+    // gqa_attention_cuda_test.cpp:259-357: one history token and two current
+    // tokens through KvCache, then attention over the cache views.
+    std::vector<uint16_t> att_values(std::size_t count, float scale, int offset)
+    {
+        std::vector<uint16_t> out(count);
+        for (std::size_t i = 0; i < count; ++i)
+            out[i] = q3o_bf16_from_f32(static_cast<float>(static_cast<int>((i + offset) % 11) - 5) * scale);
+        return out;
+    }
+
+    void attention_scenario()
+    {
+        constexpr std::int64_t B = 2, S = 2, start = 1, cap = 4;
+        constexpr std::int32_t Hq = 4, Hkv = 2, D = 4;
+        KvCache cache{1, B, cap, Hkv, D, DType::BFloat16, qwen3::Device::cuda(0)};
+        const auto hk = att_values(B * Hkv * D, 0.125F, 1), hv = att_values(B * Hkv * D, 0.25F, 2);
+        const auto ck = att_values(B * S * Hkv * D, 0.125F, 3), cv = att_values(B * S * Hkv * D, 0.25F, 4);
+        const auto q = att_values(B * S * Hq * D, 0.125F, 5);
+        cache.append(0, 0, test::to_gpu(hk, Shape{B, 1, Hkv * D}, DType::BFloat16),
+                     test::to_gpu(hv, Shape{B, 1, Hkv * D}, DType::BFloat16));
+        cache.append(0, start, test::to_gpu(ck, Shape{B, S, Hkv * D}, DType::BFloat16),
+                     test::to_gpu(cv, Shape{B, S, Hkv * D}, DType::BFloat16));
+        Tensor qt = test::to_gpu(q, Shape{B, S, Hq * D}, DType::BFloat16);
+        const auto kview = cache.key_view(0), vview = cache.value_view(0);
+        Tensor out = qwen3::ops::grouped_query_attention(qt, kview, vview, Hq, start);
+        require(out.shape() == qt.shape(), "attention output shape");
+        const auto got = test::to_host<uint16_t>(out);
+        // the oracle over the cache storage, with the view's strides
+        const auto ks = test::to_host<uint16_t>(cache.key_storage()), vs = test::to_host<uint16_t>(cache.value_storage());
+        const std::int64_t st[4] = {cap * Hkv * D, Hkv * D, D, 1};
+        std::vector<uint16_t> prim(got.size()), lo(got.size()), hi(got.size());
+        require(q3o_gqa_attention(q.data(), ks.data(), vs.data(), B, S, Hq, Hkv, D, start + S, start, st, st, nullptr, 0,
+                                  prim.data(), lo.data(), hi.data(), 2) == 0,
+                "oracle attention");
+        for (std::size_t i = 0; i < got.size(); ++i)
+            require(std::fabs(q3o_f32_from_bf16(got[i]) - q3o_f32_from_bf16(prim[i])) <= 0.04F,
+                    "attention within the reference test's tolerance");
+        test::require_band(got, prim, lo, hi, "attention");
+        // the reference's checks
+        require_throws<std::invalid_argument>([&] { (void)qwen3::ops::grouped_query_attention(qt, kview, vview, Hq, 0); },
+                                              "cache length not start + S accepted");
+        require_throws<std::invalid_argument>([&] { (void)qwen3::ops::grouped_query_attention(qt, kview, vview, 3, start); },
+                                              "query heads not divisible by KV heads accepted");
+    }
+
     void body()
     {
         test::require_gpu();
@@ -161,6 +208,7 @@ namespace
         reference_scenario();
         fp32_cache();
         fused_append();
+        attention_scenario();
         require(test::current_device() == before, "a KV cache call changed the current device");
     }
 } // namespace

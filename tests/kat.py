@@ -72,3 +72,26 @@ def kv_steps():
     dec = (KV_BATCH, 1, P)
     return [(0, kv_values(int(np.prod(pre)), 1.0).reshape(pre), kv_values(int(np.prod(pre)), 21.0).reshape(pre)),
             (2, kv_values(int(np.prod(dec)), 41.0).reshape(dec), kv_values(int(np.prod(dec)), 61.0).reshape(dec))]
+
+
+# GQA attention KAT (gqa_attention_cuda_test.cpp:259-357): B 2, S 2 at start 1 (3 cached), 4 query heads over 2 KV
+# heads of dim 4; value i of each tensor is ((i + offset) % 11 - 5) * scale; tolerance 0.04 (:239-257)
+ATT_B, ATT_S, ATT_START, ATT_HQ, ATT_HKV, ATT_D, ATT_TOL = 2, 2, 1, 4, 2, 4, 0.04
+
+
+def att_values(count, scale, offset):
+    i = np.arange(count)
+    return bf((((i + offset) % 11) - 5) * scale)
+
+
+def att_inputs():
+    """(query [B,S,Hq*D], keys [B,3,Hkv,D], values [B,3,Hkv,D]) of the test: one history token then the 2 current."""
+    B, S, P = ATT_B, ATT_S, ATT_HKV * ATT_D
+    hk = att_values(B * 1 * P, 0.125, 1).reshape(B, 1, P)
+    hv = att_values(B * 1 * P, 0.25, 2).reshape(B, 1, P)
+    ck = att_values(B * S * P, 0.125, 3).reshape(B, S, P)
+    cv = att_values(B * S * P, 0.25, 4).reshape(B, S, P)
+    q = att_values(B * S * ATT_HQ * ATT_D, 0.125, 5).reshape(B, S, ATT_HQ * ATT_D)
+    keys = np.concatenate([hk, ck], axis=1).reshape(B, 1 + S, ATT_HKV, ATT_D)
+    vals = np.concatenate([hv, cv], axis=1).reshape(B, 1 + S, ATT_HKV, ATT_D)
+    return q, keys, vals

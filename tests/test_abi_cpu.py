@@ -120,3 +120,33 @@ def test_caller_fusion_argument_errors(q3k):
     _expect(q3k.embedding_rms_norm, ValueError, IA, fake, 4, fake, 10, 1024, fake, 0.0, fake, fake)
     q3k.rms_norm_rows(None, None, None, 0, 0, 1, 1024, 1e-6)
     q3k.embedding_rms_norm(None, 0, None, 10, 1024, None, 1e-6, None, None)
+
+
+def test_kv_and_attention_argument_errors(q3k):
+    IA, OR, OV = q3k.Q3K_ERR_INVALID_ARGUMENT, q3k.Q3K_ERR_OUT_OF_RANGE, q3k.Q3K_ERR_OVERFLOW
+    fake = 256
+    # KV append: capacity (kv_cache.cpp:121-125), sizes, null pointers
+    msg = _expect(q3k.kv_append, IndexError, OR, fake, fake, fake, fake, 2, 5, 2048, 8, 4)
+    assert "capacity" in msg
+    _expect(q3k.kv_append, ValueError, IA, fake, fake, fake, fake, -1, 5, 2048, 8, 0)
+    _expect(q3k.kv_append, ValueError, IA, fake, fake, fake, fake, 2, 5, 0, 8, 0)
+    _expect(q3k.kv_append, ValueError, IA, None, fake, fake, fake, 2, 5, 2048, 8, 0)
+    _expect(q3k.kv_append, OverflowError, OV, fake, fake, fake, fake, 2**40, 1, 2**20, 2**10, 0)
+    q3k.kv_append(None, None, None, None, 0, 5, 2048, 8, 0)
+    # fused Q/K norm + RoPE + append: RoPE range first, then the cache capacity
+    _expect(q3k.qk_norm_rope_kv_append, IndexError, OR, fake, fake, fake, fake, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 14,
+            fake, fake, 64, 0)
+    _expect(q3k.qk_norm_rope_kv_append, IndexError, OR, fake, fake, fake, fake, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 0,
+            fake, fake, 4, 2)
+    _expect(q3k.qk_norm_rope_kv_append, ValueError, IA, fake, fake, None, fake, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 0,
+            fake, fake, 8, 0)
+    # attention (gqa_attention.cu:157-302)
+    st = (64, 16, 8, 1)
+    msg = _expect(q3k.gqa_attention, ValueError, IA, fake, fake, fake, fake, 1, 2, 4, 2, 8, 5, 1, st, st)
+    assert "start_position + sequence_length" in msg
+    _expect(q3k.gqa_attention, ValueError, IA, fake, fake, fake, fake, 1, 2, 3, 2, 8, 3, 1, st, st)
+    _expect(q3k.gqa_attention, ValueError, IA, fake, fake, fake, fake, 1, 2, 4, 2, 512, 3, 1, st, st)
+    _expect(q3k.gqa_attention, ValueError, IA, fake, fake, fake, fake, 1, 2, 4, 2, 8, 1, -1, st, st)
+    _expect(q3k.gqa_attention, ValueError, IA, None, fake, fake, fake, 1, 2, 4, 2, 8, 3, 1, st, st)
+    _expect(q3k.gqa_attention, OverflowError, OV, fake, fake, fake, fake, 2**20, 2**10, 4, 2, 8, 2**10, 0, st, st)
+    q3k.gqa_attention(None, None, None, None, 0, 2, 4, 2, 8, 3, 1, st, st)

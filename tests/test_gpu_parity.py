@@ -478,3 +478,78 @@ def test_qk_norm_rope_kv_append(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, Sc, c
     hip.synchronize()
     check_exact(name + " q == qk_norm_rope", got_q, Q2.get(np.uint16, q.shape))
     check_exact(name + " k cache == qk_norm_rope + kv_append", got_kc, KC2.get(np.uint16, kc0.shape))
+
+
+# ---------------------------------------------------------------- attention
+
+def run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, offset=0):
+    """q [B, S, Hq * D]; the caches are whole KvCache-like layers [Bcap, Scap, Hkv, D], read through the
+    [B, start + S] view (strides of the storage), as KvCache::key_view hands them over."""
+    _, Scap, Hkv, D = store_k.shape
+    Q, K, V = Guarded(hip, q, offset=offset), Guarded(hip, store_k, offset=offset), Guarded(hip, store_v, offset=offset)
+    O = Guarded(hip, nbytes=q.nbytes, offset=offset)
+    st = (Scap * Hkv * D, Hkv * D, D, 1)
+    q3k.gqa_attention(Q, K, V, O, B, S, Hq, Hkv, D, start + S, start, st, st)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (Q, K, V, O))
+    assert np.array_equal(Q.get(np.uint16, q.shape), q) and np.array_equal(K.get(np.uint16, store_k.shape), store_k)
+    return O.get(np.uint16, q.shape)
+
+
+def test_attention_kat(q3k, hip, oracle):
+    """gqa_attention_cuda_test.cpp:259-357: 1 history token + 2 current into a capacity-4 cache, 4 query heads over
+    2 KV heads of dim 4, checked at the test's tolerance and against the oracle band."""
+    announce("gqa_attention KAT")
+    q, kc, vc = kat.att_inputs()
+    B, S = kat.ATT_B, kat.ATT_S
+    store_k = np.zeros((B, 4, kat.ATT_HKV, kat.ATT_D), np.uint16)
+    store_v = np.zeros_like(store_k)
+    store_k[:, :3], store_v[:, :3] = kc, vc
+    got = run_attention(q3k, hip, q, store_k, store_v, B, S, kat.ATT_HQ, kat.ATT_START)
+    prim, lo, hi = oracle.gqa_attention(q, kc, vc, kat.ATT_HQ, kat.ATT_START)
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+    assert np.all(np.abs(f(got) - f(prim)) <= kat.ATT_TOL)
+    check_band(oracle, "gqa_attention KAT", got, prim, lo, hi)
+
+
+@pytest.mark.parametrize("B,S,start,Hq,Hkv,D,cap,offset", [
+    (2, 40, 0, 32, 8, 128, 64, 0),      # Qwen3-8B heads, prefill (G = 4)
+    (1, 77, 13, 16, 8, 128, 100, 0),    # G = 2, partial tiles, prefix in the cache
+    (8, 1, 300, 32, 8, 128, 512, 0),    # decode step
+    (2, 33, 5, 8, 8, 128, 40, 0),       # G = 1
+    (1, 10, 0, 64, 8, 128, 10, 0),      # Qwen3-32B grouping (G = 8)
+    (1, 9, 3, 32, 2, 128, 12, 0),       # G = 16
+    (1, 5, 60, 32, 1, 128, 65, 0),      # G = 32
+    (2, 21, 4, 8, 2, 64, 32, 0),        # head_dim 64: generic kernel
+    (1, 12, 3, 8, 2, 128, 16, 2),       # unaligned caches: generic kernel
+    (1, 6, 0, 4, 4, 256, 6, 0),         # head_dim 256: generic kernel
+])
+def test_gqa_attention(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, D, cap, offset):
+    name = f"gqa_attention B={B} S={S} start={start} Hq={Hq} Hkv={Hkv} D={D} cap={cap} offset={offset}"
+    announce(name)
+    q = synth.normal_bf16(160, S, (B, S, Hq * D))
+    store_k = synth.normal_bf16(161, S, (B + 1, cap, Hkv, D))
+    store_v = synth.normal_bf16(162, S, (B + 1, cap, Hkv, D))
+    got = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, offset=offset)
+    prim, lo, hi = oracle.gqa_attention(q, store_k[:B, :start + S], store_v[:B, :start + S], Hq, start)
+    check_band(oracle, name, got, prim, lo, hi)
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
+def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
+    """Benchmark-size prefill (config 4 shape, and a 4096-token sequence): every row computed on the GPU, a seeded
+    sample of rows (always including the last positions, the longest contexts) checked against the oracle."""
+    D = 128
+    name = f"gqa_attention prefill B={B} S={S} Hq={Hq} Hkv={Hkv} rows={nrows}"
+    announce(name)
+    q = synth.normal_bf16(163, S, (B, S, Hq * D))
+    store_k = synth.normal_bf16(164, S, (B, S, Hkv, D))
+    store_v = synth.normal_bf16(165, S, (B, S, Hkv, D))
+    got = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, 0)
+    rng = np.random.default_rng(S)
+    total = B * S * Hq
+    rows = np.unique(np.concatenate([rng.integers(0, total, nrows - 2 * Hq),
+                                     np.arange(total - Hq, total), np.arange(S * Hq - Hq, S * Hq)]))
+    prim, lo, hi = oracle.gqa_attention(q, store_k, store_v, Hq, 0, rows=rows)
+    check_band(oracle, name, got.reshape(-1, D)[rows], prim, lo, hi)
+    assert np.isfinite(synth.bf16_to_f32(got)).all()

@@ -387,3 +387,109 @@ def test_kv_append_fp32_rows_and_bytes(oracle, synth):
     assert np.array_equal(kc2[:3, 5:9].view(np.uint32), k.view(np.uint32))
     assert np.array_equal(vc2[:3, 5:9].view(np.uint32), v.view(np.uint32))
     assert np.isnan(kc2[3]).all() and np.isnan(kc2[:, :5]).all() and np.isnan(vc2[:, :5]).all()
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_f64(q, kc, vc, Hq, start):
+    """Causal GQA attention in float64 with torch SDPA (head h reads KV head h // G, as HF Qwen3 repeat_kv)."""
+    B, S = q.shape[:2]
+    _, L, Hkv, D = kc.shape
+    G = Hq // Hkv
+    f = lambda b: torch.from_numpy((b.astype(np.uint32) << 16).view(np.float32).astype(np.float64))  # noqa: E731
+    qt = f(np.ascontiguousarray(q)).reshape(B, S, Hq, D).transpose(1, 2)
+    kt = f(np.ascontiguousarray(kc)).transpose(1, 2).repeat_interleave(G, dim=1)
+    vt = f(np.ascontiguousarray(vc)).transpose(1, 2).repeat_interleave(G, dim=1)
+    pos_q = start + torch.arange(S)[:, None]
+    mask = torch.arange(L)[None, :] <= pos_q
+    o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask,
+                                                         scale=float(np.float32(1.0) / np.sqrt(np.float32(D))))
+    return o.transpose(1, 2).reshape(B, S, Hq * D).numpy()
+
+
+def test_attention_kat(oracle):
+    """The reference test's case and its tolerance; its own expected values are a two-pass fp32 softmax
+    (gqa_attention_cuda_test.cpp:117-236), restated here in numpy."""
+    q, kc, vc = kat.att_inputs()
+    prim, lo, hi = oracle.gqa_attention(q, kc, vc, kat.ATT_HQ, kat.ATT_START)
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+    B, S, Hq, Hkv, D = kat.ATT_B, kat.ATT_S, kat.ATT_HQ, kat.ATT_HKV, kat.ATT_D
+    qf, kf, vf = f(q).reshape(B, S, Hq, D), f(kc), f(vc)
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    for b in range(B):
+        for s in range(S):
+            vis = kat.ATT_START + s + 1
+            for h in range(Hq):
+                g = h // (Hq // Hkv)
+                scores = np.array([np.float32(np.sum(qf[b, s, h] * kf[b, j, g], dtype=np.float32)) * scale
+                                   for j in range(vis)], np.float32)
+                w = np.exp(scores - scores.max()).astype(np.float32)
+                ref = (w[:, None] / w.sum(dtype=np.float32) * vf[b, :vis, g]).sum(axis=0, dtype=np.float32)
+                got = f(prim[b, s, h * D:(h + 1) * D])
+                assert np.all(np.abs(got - ref) <= kat.ATT_TOL), (b, s, h, got, ref)
+    assert oracle.compare(prim, prim, lo, hi)["fail"] == 0
+
+
+def test_attention_matches_float64_sdpa(oracle, synth):
+    """An independent implementation (torch SDPA in float64): its rounded values lie in the band, and the primary
+    result is within one ulp of them; GQA head grouping, causal offset and strided cache views included."""
+    B, S, Hq, Hkv, D, start, cap = 2, 24, 8, 2, 128, 40, 80
+    q = synth.normal_bf16(140, 1, (B, S, Hq * D))
+    store_k = synth.normal_bf16(141, 1, (B + 1, cap, Hkv, D))
+    store_v = synth.normal_bf16(142, 1, (B + 1, cap, Hkv, D))
+    kc, vc = store_k[:B, :start + S], store_v[:B, :start + S]  # strided views, as KvCache::key_view
+    prim, lo, hi = oracle.gqa_attention(q, kc, vc, Hq, start)
+    ref = synth.f32_to_bf16(_attn_f64(q, kc, vc, Hq, start).astype(np.float32))
+    st = oracle.compare(ref, prim, lo, hi)
+    assert st["fail"] == 0, st
+    st2 = oracle.compare(prim, ref)
+    assert st2["fail"] == 0 and st2["n"] == prim.size, st2  # primary within 1 ulp of the float64 result
+    assert st["ambiguous"] <= 0.12 * prim.size, st          # the band stays narrow
+
+
+def test_attention_closed_forms(oracle, synth):
+    D, Hq, Hkv = 128, 4, 2
+    # one visible key (start 0, position 0): the output is that value row, bit for bit
+    q = synth.normal_bf16(143, 1, (1, 1, Hq * D))
+    kc = synth.normal_bf16(144, 1, (1, 1, Hkv, D))
+    vc = synth.normal_bf16(145, 1, (1, 1, Hkv, D))
+    prim, _, _ = oracle.gqa_attention(q, kc, vc, Hq, 0)
+    assert np.array_equal(prim.reshape(Hq, D), vc[0, 0, np.arange(Hq) // 2])
+    # identical keys: uniform weights, the output is the mean of the visible values
+    L = 37
+    k1 = np.broadcast_to(synth.normal_bf16(146, 1, (1, 1, Hkv, D)), (1, L, Hkv, D)).copy()
+    vL = synth.normal_bf16(147, 1, (1, L, Hkv, D))
+    qL = synth.normal_bf16(148, 1, (1, 1, Hq * D))
+    prim, lo, hi = oracle.gqa_attention(qL, k1, vL, Hq, L - 1)
+    mean = synth.bf16_to_f32(vL).astype(np.float64).mean(axis=1)[0]          # [Hkv, D]
+    want = synth.f32_to_bf16(mean[np.arange(Hq) // 2].reshape(1, 1, Hq * D).astype(np.float32))
+    assert oracle.compare(want, prim, lo, hi)["fail"] == 0
+    # one dominant key: weight 1 on it (others underflow), the output is its value row
+    kd = synth.normal_bf16(149, 1, (1, L, Hkv, D))
+    qd = np.full((1, 1, Hq * D), synth.f32_to_bf16(np.array([2.0], np.float32))[0], np.uint16)
+    kd[0, 11] = synth.f32_to_bf16(np.array([8.0], np.float32))[0]
+    prim, _, _ = oracle.gqa_attention(qd, kd, vL, Hq, L - 1)
+    assert np.array_equal(prim.reshape(Hq, D), vL[0, 11, np.arange(Hq) // 2])
+
+
+def test_attention_row_subset_and_planted_mistake(oracle, synth):
+    B, S, Hq, Hkv, D = 1, 16, 8, 2, 128
+    q = synth.normal_bf16(150, 1, (B, S, Hq * D))
+    kc = synth.normal_bf16(151, 1, (B, S, Hkv, D))
+    vc = synth.normal_bf16(152, 1, (B, S, Hkv, D))
+    full, lo, hi = oracle.gqa_attention(q, kc, vc, Hq, 0)
+    rows = np.array([0, 5, 77, 127])
+    sub, slo, shi = oracle.gqa_attention(q, kc, vc, Hq, 0, rows=rows)
+    assert np.array_equal(sub, full.reshape(-1, D)[rows])
+    # a restatement that maps query head h to KV head h % Hkv (instead of h // G) is rejected by the rule
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)  # noqa: E731
+    qf = f(q).reshape(S, Hq, D)
+    out = np.empty((S, Hq, D))
+    for s in range(S):
+        for h in range(Hq):
+            g = h % Hkv
+            sc = (f(kc[0, :s + 1, g]) @ qf[s, h]) * float(np.float32(1) / np.sqrt(np.float32(D)))
+            w = np.exp(sc - sc.max())
+            out[s, h] = (w / w.sum()) @ f(vc[0, :s + 1, g])
+    wrong = synth.f32_to_bf16(out.astype(np.float32)).reshape(B, S, Hq * D)
+    assert oracle.compare(wrong, full, lo, hi)["fail"] > 0
