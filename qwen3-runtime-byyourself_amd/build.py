@@ -42,6 +42,9 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-fvisibility=hidden", "-Wall", "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs: the attention loop rescales
+    # them with VALU ops, and AGPR copies would cost ~128 moves per key tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE_DIR}",
 ]
 CXX_FLAGS = [

@@ -6,11 +6,12 @@
 // Matrix-core path (head_dim 128, unit dim stride, 16-byte rows): a block of
 // four waves owns one (batch, KV head) and QP query positions of all G heads
 // of that group, so every K/V tile it stages in LDS serves G heads.  A wave's
-// 32 "columns" are (position, head) pairs.  Per tile of 32 keys:
+// 32 "columns" are (position, head) pairs.  Per 32 keys:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16: A = K rows from LDS,
 //                 B = the wave's Q fragments (registers for the whole loop);
 //   online softmax per column: a lane holds one column, so the key max and
-//                 sum need only its 16 registers and the lane 32 apart;
+//                 sum need only its own registers and the lane 32 apart
+//                 (v_permlane32_swap);
 //   O^T += V^T P^T: A = V^T from a transposed LDS copy of the tile, B = P^T
 //                 straight from the S^T registers.  P is split into a bf16
 //                 high part and a bf16 remainder (two MFMAs), so the weights
@@ -18,8 +19,9 @@
 //                 p * v in fp32, and a single bf16 rounding of p would cost
 //                 up to half an output ulp.
 // Scores are scaled by scale * log2(e) and exponentiated with v_exp_f32.
-// The next tile's K and V are loaded into registers while the current one
-// is computed.
+// Keys go in tiles of 64 (two S^T halves of 32): a tile's K and V are loaded
+// into registers while the previous tile is computed, then stored to the
+// other of two LDS buffers, one barrier per tile.
 //
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
 // keys in order, lanes over the head dimension -- the reference's own
@@ -34,11 +36,12 @@ namespace q3k
         typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
         constexpr int kAttD = 128;
-        constexpr int kKeyTile = 32;
-        constexpr int kKRowBytes = kAttD * 2 + 16;   // K tile row in LDS, padded: conflict-free b128 reads
+        constexpr int kKeyTile = 64;                   // keys per pipeline step
+        constexpr int kKRowBytes = kAttD * 2 + 16;     // K tile row in LDS, padded: conflict-free b128 reads
         constexpr int kVtRowBytes = kKeyTile * 2 + 16; // V^T tile row (one head-dim index), padded likewise
         constexpr int kKTileBytes = kKeyTile * kKRowBytes;
         constexpr int kVtTileBytes = kAttD * kVtRowBytes;
+        constexpr int kTileBytes = kKTileBytes + kVtTileBytes;
         constexpr float kLog2e = 1.4426950408889634f;
 
         struct AttnArgs
@@ -60,10 +63,10 @@ namespace q3k
 
         __device__ __forceinline__ bf16x8_t as_bf8(const Vec8 &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-        // LDS position of key kk (0..31) in a V^T row: bits 2 and 3 swapped, so
-        // that the 8 keys lane group g feeds to the PV MFMA of chunk m (keys
-        // 16m + 8h + 4g + j, h < 2, j < 4: the S^T accumulator rows the lane
-        // holds) are 8 consecutive positions 16m + 8g .. + 7.
+        // LDS position of key kk (0..63) in a V^T row.  Within each half of 32
+        // keys, bits 2 and 3 are swapped, so that the 8 keys lane group g feeds
+        // to the PV MFMA of chunk m (keys 16m + 8h + 4g + j, h < 2, j < 4: the
+        // S^T accumulator rows the lane holds) are 8 consecutive positions.
         __device__ __forceinline__ int vt_pos(int kk) { return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1); }
 
         __device__ __forceinline__ uint32_t bf_pair(uint32_t lo_word, uint32_t hi_word, int half)
@@ -72,14 +75,27 @@ namespace q3k
             return half == 0 ? ((lo_word & 0xffffu) | (hi_word << 16)) : ((lo_word >> 16) | (hi_word & 0xffff0000u));
         }
 
+        // max / sum of x over lanes l and l ^ 32, in every lane (one VALU swap,
+        // no LDS): after the swap one operand is x and the other its partner
+        __device__ __forceinline__ float pair_max(float x)
+        {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+            return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+        }
+        __device__ __forceinline__ float pair_sum(float x)
+        {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+            return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+
         template <int G>
         __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a)
         {
             constexpr int PW = 32 / G; // query positions per wave
             constexpr int QP = 4 * PW; // per block
-            __shared__ __attribute__((aligned(16))) unsigned char lds[kKTileBytes + kVtTileBytes];
-            unsigned char *k_lds = lds;
-            unsigned char *vt_lds = lds + kKTileBytes;
+            // two buffers: tile t is read from buffer t % 2 while tile t + 1 is
+            // staged from registers into the other after the compute
+            __shared__ __attribute__((aligned(16))) unsigned char lds[2][kTileBytes];
 
             const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             const int lane = threadIdx.x % kWave;
@@ -91,23 +107,25 @@ namespace q3k
             bid /= a.qblocks;
             const int kvh = bid % a.Hkv;
             const int64_t b = bid / a.Hkv;
-            const int64_t s0 = static_cast<int64_t>(qb) * QP;
-            const int64_t s_last = (s0 + QP < a.S ? s0 + QP : a.S) - 1;
-            const int64_t n_keys = a.start + s_last + 1;
-            const int ntiles = static_cast<int>((n_keys + kKeyTile - 1) / kKeyTile);
+            // positions and key indices fit in 32 bits (checked by the launcher)
+            const int32_t S = static_cast<int32_t>(a.S), start = static_cast<int32_t>(a.start);
+            const int32_t s0 = qb * QP;
+            const int32_t s_last = (s0 + QP < S ? s0 + QP : S) - 1;
+            const int32_t n_keys = start + s_last + 1;
+            const int ntiles = (n_keys + kKeyTile - 1) / kKeyTile;
 
             // this lane's column
-            const int64_t wave_s0 = s0 + wave * PW;
-            const int64_t s_col = wave_s0 + li / G;
+            const int32_t wave_s0 = s0 + wave * PW;
+            const int32_t s_col = wave_s0 + li / G;
             const int h_col = kvh * G + li % G;
-            const bool col_ok = s_col < a.S;
-            const int64_t last_key = a.start + s_col;
-            const bool wave_active = wave_s0 < a.S;
-            const bool wave_partial = wave_s0 + PW > a.S;
+            const bool col_ok = s_col < S;
+            const int32_t last_key = start + s_col;
+            const bool wave_active = wave_s0 < S;
+            const bool wave_partial = wave_s0 + PW > S;
 
             bf16x8_t qf[kAttD / 16];
             {
-                const Vec8 *qrow = reinterpret_cast<const Vec8 *>(a.q + ((b * a.S + s_col) * a.Hq + h_col) * kAttD);
+                const Vec8 *qrow = reinterpret_cast<const Vec8 *>(a.q + ((b * S + s_col) * a.Hq + h_col) * kAttD);
                 const Vec8 zero = {{0u, 0u, 0u, 0u}};
 #pragma unroll
                 for (int c = 0; c < kAttD / 16; ++c)
@@ -116,38 +134,46 @@ namespace q3k
 
             const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;
             const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;
-            // staging: K chunks (key = id / 16, 16-byte chunk id % 16 of the row), V key pair x 8 dims
-            const int k_key0 = threadIdx.x / 16, k_chunk = threadIdx.x % 16;
+            // staging: K rows k_row + 16 x (x < 4), 16-byte chunk k_chunk of each;
+            // V key pairs v_pair and v_pair + 16 (keys 2p, 2p + 1), dims 8 v_chunk .. + 7
+            const int k_row = threadIdx.x / 16, k_chunk = threadIdx.x % 16;
             const int v_chunk = threadIdx.x / 16, v_pair = threadIdx.x % 16;
-            Vec8 kst[2], vst[2];
+            Vec8 kst[4], vst[4];
             auto load_tile = [&](int tile) {
-                const int64_t key0 = static_cast<int64_t>(tile) * kKeyTile;
+                const int32_t key0 = tile * kKeyTile;
                 const Vec8 zero = {{0u, 0u, 0u, 0u}};
 #pragma unroll
-                for (int x = 0; x < 2; ++x)
+                for (int x = 0; x < 4; ++x)
                 {
-                    const int64_t key = key0 + k_key0 + 16 * x;
+                    const int32_t key = key0 + k_row + 16 * x;
                     kst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(kbase + key * a.ks1) + k_chunk)
                                           : zero;
                 }
 #pragma unroll
-                for (int x = 0; x < 2; ++x)
+                for (int x = 0; x < 4; ++x)
                 {
-                    const int64_t key = key0 + 2 * v_pair + x;
+                    const int32_t key = key0 + 2 * (v_pair + 16 * (x / 2)) + x % 2;
                     vst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(vbase + key * a.vs1) + v_chunk)
                                           : zero;
                 }
             };
-            auto store_tile = [&]() {
+            auto store_tile = [&](unsigned char *buf) {
+                unsigned char *k_lds = buf;
+                unsigned char *vt_lds = buf + kKTileBytes;
 #pragma unroll
-                for (int x = 0; x < 2; ++x)
-                    *reinterpret_cast<Vec8 *>(k_lds + (k_key0 + 16 * x) * kKRowBytes + k_chunk * 16) = kst[x];
-                const int pos = vt_pos(2 * v_pair);
+                for (int x = 0; x < 4; ++x)
+                    *reinterpret_cast<Vec8 *>(k_lds + (k_row + 16 * x) * kKRowBytes + k_chunk * 16) = kst[x];
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
+                for (int y = 0; y < 2; ++y)
                 {
-                    const uint32_t w = bf_pair(vst[0].d[e / 2], vst[1].d[e / 2], e % 2);
-                    *reinterpret_cast<uint32_t *>(vt_lds + (8 * v_chunk + e) * kVtRowBytes + pos * 2) = w;
+                    const int kk = 2 * (v_pair + 16 * y);
+                    const int pos = (kk & 32) | vt_pos(kk & 31);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                    {
+                        const uint32_t w = bf_pair(vst[2 * y].d[e / 2], vst[2 * y + 1].d[e / 2], e % 2);
+                        *reinterpret_cast<uint32_t *>(vt_lds + (8 * v_chunk + e) * kVtRowBytes + pos * 2) = w;
+                    }
                 }
             };
 
@@ -159,94 +185,114 @@ namespace q3k
             const float scale2 = a.scale * kLog2e;
 
             load_tile(0);
+            store_tile(lds[0]);
+            __syncthreads();
             for (int tile = 0; tile < ntiles; ++tile)
             {
-                __syncthreads(); // the previous tile has been consumed
-                store_tile();
-                __syncthreads();
-                if (tile + 1 < ntiles)
-                    load_tile(tile + 1);
-                if (!wave_active)
-                    continue;
-                const int64_t key0 = static_cast<int64_t>(tile) * kKeyTile;
+                const bool more = tile + 1 < ntiles;
+                if (more)
+                    load_tile(tile + 1); // in flight while this tile is computed
+                const unsigned char *k_lds = lds[tile % 2];
+                const unsigned char *vt_lds = lds[tile % 2] + kKTileBytes;
+                if (wave_active)
+                {
+                    const int32_t key0 = tile * kKeyTile;
+                    f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+                    for (int c = 0; c < kAttD / 16; ++c)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+                        {
+                            const Vec8 kf = *reinterpret_cast<const Vec8 *>(k_lds + (32 * hh + li) * kKRowBytes +
+                                                                             (16 * c + 8 * lg) * 2);
+                            sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kf), qf[c], sacc[hh], 0, 0, 0);
+                        }
 
-                f32x16_t sacc = f32x16_t{};
-#pragma unroll
-                for (int c = 0; c < kAttD / 16; ++c)
-                {
-                    const Vec8 kf = *reinterpret_cast<const Vec8 *>(k_lds + li * kKRowBytes + (16 * c + 8 * lg) * 2);
-                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kf), qf[c], sacc, 0, 0, 0);
-                }
-
-                const bool need_mask = key0 + kKeyTile - 1 > a.start + wave_s0 || wave_partial;
-                float sc[16];
-                float mloc = -__builtin_huge_valf();
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                {
-                    float x = sacc[r] * scale2;
-                    if (need_mask)
+                    // Masked scores become -inf before the max; the max of the raw
+                    // scores times the (positive) scale is the max of the scaled ones.
+                    if (key0 + kKeyTile - 1 > start + wave_s0 || wave_partial)
                     {
-                        const int64_t kk = key0 + 8 * (r / 4) + 4 * lg + (r % 4);
-                        if (kk > last_key || !col_ok)
-                            x = -__builtin_huge_valf();
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                            {
+                                const int32_t kk = key0 + 32 * hh + 8 * (r / 4) + 4 * lg + (r % 4);
+                                if (kk > last_key || !col_ok)
+                                    sacc[hh][r] = -__builtin_huge_valf();
+                            }
                     }
-                    sc[r] = x;
-                    mloc = fmaxf(mloc, x);
-                }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-                const float m_new = fmaxf(m, mloc);
-                const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-                float p[16];
-                float psum = 0.0f;
+                    float mloc = sacc[0][0];
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                {
-                    p[r] = __builtin_amdgcn_exp2f(sc[r] - m_use);
-                    psum += p[r];
-                }
-                psum += __shfl_xor(psum, 32);
-                l = l * alpha + psum;
-                m = m_new;
+                    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int dt = 0; dt < kAttD / 32; ++dt)
+                        for (int r = 0; r < 16; ++r)
+                            mloc = fmaxf(mloc, sacc[hh][r]);
+                    mloc = pair_max(mloc);
+                    const float m_new = fmaxf(m, mloc * scale2);
+                    const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
+                    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+                    bf16x8_t phi[2][2], plo[2][2];
+                    float psum = 0.0f;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        o[dt][r] *= alpha;
-
-                bf16x8_t phi[2], plo[2];
+                    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int mm = 0; mm < 2; ++mm)
-                {
-                    Vec8 h8, l8;
+                        for (int mm = 0; mm < 2; ++mm)
+                        {
+                            Vec8 h8, l8;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                            for (int j = 0; j < 4; ++j)
+                            {
+                                const float x0 = __builtin_amdgcn_exp2f(
+                                    __builtin_fmaf(sacc[hh][8 * mm + 2 * j], scale2, -m_use));
+                                const float x1 = __builtin_amdgcn_exp2f(
+                                    __builtin_fmaf(sacc[hh][8 * mm + 2 * j + 1], scale2, -m_use));
+                                psum += x0;
+                                psum += x1;
+                                const uint32_t hp = pack_rne(x0, x1);
+                                h8.d[j] = hp;
+                                l8.d[j] = pack_rne(x0 - bf_lo(hp), x1 - bf_hi(hp));
+                            }
+                            phi[hh][mm] = as_bf8(h8);
+                            plo[hh][mm] = as_bf8(l8);
+                        }
+                    psum = pair_sum(psum);
+                    l = l * alpha + psum;
+                    m = m_new;
+                    // the running max rarely moves after the first tiles: multiplying
+                    // by alpha == 1 changes nothing, so the wave skips it then
+                    if (__any(alpha != 1.0f))
                     {
-                        const float x0 = p[8 * mm + 2 * j], x1 = p[8 * mm + 2 * j + 1];
-                        const uint32_t hp = pack_rne(x0, x1);
-                        h8.d[j] = hp;
-                        l8.d[j] = pack_rne(x0 - bf_lo(hp), x1 - bf_hi(hp));
+#pragma unroll
+                        for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                o[dt][r] *= alpha;
                     }
-                    phi[mm] = as_bf8(h8);
-                    plo[mm] = as_bf8(l8);
+#pragma unroll
+                    for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                            for (int mm = 0; mm < 2; ++mm)
+                            {
+                                const Vec8 vf = *reinterpret_cast<const Vec8 *>(
+                                    vt_lds + (dt * 32 + li) * kVtRowBytes + (32 * hh + 16 * mm + 8 * lg) * 2);
+                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), phi[hh][mm], o[dt], 0, 0,
+                                                                                0);
+                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), plo[hh][mm], o[dt], 0, 0,
+                                                                                0);
+                            }
                 }
-#pragma unroll
-                for (int dt = 0; dt < kAttD / 32; ++dt)
-#pragma unroll
-                    for (int mm = 0; mm < 2; ++mm)
-                    {
-                        const Vec8 vf = *reinterpret_cast<const Vec8 *>(vt_lds + (dt * 32 + li) * kVtRowBytes +
-                                                                         (16 * mm + 8 * lg) * 2);
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), phi[mm], o[dt], 0, 0, 0);
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), plo[mm], o[dt], 0, 0, 0);
-                    }
+                if (more)
+                    store_tile(lds[(tile + 1) % 2]);
+                __syncthreads(); // tile + 1 is staged; every wave is done with tile
             }
 
             if (!col_ok)
                 return;
             const float inv = 1.0f / l;
-            uint16_t *orow = a.out + ((b * a.S + s_col) * a.Hq + h_col) * kAttD;
+            uint16_t *orow = a.out + ((b * S + s_col) * a.Hq + h_col) * kAttD;
 #pragma unroll
             for (int dt = 0; dt < kAttD / 32; ++dt)
 #pragma unroll
@@ -323,7 +369,7 @@ namespace q3k
         bool mfma_ok(const AttnArgs &a, int32_t G)
         {
             const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32;
-            return g_ok && a.D == kAttD && a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
+            return g_ok && a.D == kAttD && a.start + a.S <= INT32_MAX && a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
                    a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 && aligned16(a.q) &&
                    aligned16(a.k) && aligned16(a.v) && aligned_to(a.out, 8);
         }
