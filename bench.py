@@ -44,6 +44,7 @@ sys.path.insert(0, REPO)
 PKG = "qwen3-runtime-byyourself_amd"
 METRIC = "HBM GB/s (% of peak) for RMSNorm/QK-norm+RoPE/SwiGLU at Qwen3-8B shapes"
 PEAK_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
 EPS = 1e-6
 D = 128
 
@@ -183,6 +184,42 @@ def time_each_op(hip, stream, sets, make_ops, reps, warmup=2, buffers=None):
         rot = op_rotation(hip, sets, buffers[name]) if buffers and name in buffers else sets
         out[name] = time_chain(hip, stream, rot, lambda s, k=k: [make_ops(s)[k]], max(reps, len(rot)), warmup)
         del rot
+    return out
+
+
+def attention_flops(B, S, start, Hq, D):
+    """Algorithmic flops of causal attention: 2 * D for Q K^T and 2 * D for P V per visible (query, key) pair."""
+    pairs = B * Hq * (S * start + S * (S + 1) // 2)
+    return 4 * D * pairs
+
+
+def time_attention(q3k, hip, synth, c, stream):
+    """Grouped-query attention over the layer's KV cache (gqa_attention.cu:304-345): prefill at the config's
+    [B, S] (matrix-core bound, reported in TFLOP/s against the 2.5 PFLOP/s bf16 peak) and a batched decode step
+    at 64 sequences x 4096 cached keys (HBM bound: the K/V cache is read once)."""
+    out = {}
+    print("[bench] timing attention", file=sys.stderr, flush=True)
+    for name, B, S, start in (("prefill", c.batch, c.seq, 0), ("decode_b64_l4096", 64, 1, 4095)):
+        L = start + S
+        q = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 40, (B, S, c.heads_q * D)))
+        kc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 41, (B, L, c.heads_kv, D)))
+        vc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 42, (B, L, c.heads_kv, D)))
+        o = hip.DeviceBuffer(B * S * c.heads_q * D * 2)
+        st = (L * c.heads_kv * D, c.heads_kv * D, D, 1)
+        ms = time_chain(hip, stream, [0], lambda _: [
+            ("attention", lambda: q3k.gqa_attention(q, kc, vc, o, B, S, c.heads_q, c.heads_kv, D, L, start, st, st,
+                                                    stream))], 10 if S > 1 else 50, 2)
+        flops = attention_flops(B, S, start, c.heads_q, D)
+        byts = 2 * B * L * c.heads_kv * D * 2 + 2 * B * S * c.heads_q * D * 2
+        rec = {"ms": round(ms, 5), "B": B, "S": S, "cached": L, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+               "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
+        if S > 1:
+            rec["pct_of_bf16_peak"] = round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
+        else:
+            rec["pct_of_hbm_peak"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_GBS, 2)
+        out["attention_" + name] = rec
+        for buf in (q, kc, vc, o):
+            buf.free()
     return out
 
 
@@ -368,6 +405,7 @@ def main():
         for e in kv_sets:
             for buf in e.values():
                 buf.free()
+        extras.update(time_attention(q3k, hip, synth, c, stream))
         if "embedding" in c.ops:
             print("[bench] timing embedding", file=sys.stderr, flush=True)
             for s in sets[1:]:

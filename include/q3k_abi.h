@@ -188,6 +188,38 @@ Q3K_API int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache,
                           q3k_stream_t stream);
 
 /*
+ * Argmax over the last dimension: out[r] = index of the largest of
+ * x[r * row_stride + 0 .. search_size - 1] (bf16), NaN counted as -inf, ties
+ * to the smaller index; int32 out [rows].  search_size in [1, row_stride]
+ * (a valid vocabulary prefix of padded logits).  Bit-exact.
+ * Replaces qwen3::ops::argmax_last_dimension, src/ops/argmax.cu:163-214
+ * (kernel :34-100), the greedy path of Sampler::sample
+ * (src/generation/sampler.cpp:288-291).
+ */
+Q3K_API int q3k_argmax_bf16(const uint16_t *x, int32_t *out, int64_t rows,
+                  int64_t row_stride, int64_t search_size,
+                  q3k_stream_t stream);
+
+/*
+ * Top-k candidates of sampling.  For each row r of logits (bf16, row_stride
+ * columns, the first search_size searched): every token whose logit is >=
+ * the k-th largest logit (ties at the k-th all kept; -0 equals +0), written
+ * as cand_index[r * cap + i] / cand_logit[r * cap + i] (bf16 bits) for
+ * i < min(count[r], cap), in no particular order; count[r] may exceed cap
+ * (then the caller falls back to the whole row).  nonfinite[r] != 0 when
+ * the searched row holds a NaN or infinity.  This is the top-k step of the
+ * reference's host sampler (temperature is monotone, so it does not change
+ * the set), src/generation/sampler.cpp:160-190, moved to the GPU so that
+ * only the candidates cross to the host (the reference copies all logits,
+ * :296-312).
+ */
+Q3K_API int q3k_topk_candidates_bf16(const uint16_t *logits, int64_t rows,
+                          int64_t row_stride, int64_t search_size, int32_t k,
+                          int32_t cap, int32_t *count, int32_t *cand_index,
+                          uint16_t *cand_logit, int32_t *nonfinite,
+                          q3k_stream_t stream);
+
+/*
  * KV-cache append: K and V [B, S, row_bytes] (contiguous) are copied to rows
  * start .. start + S - 1 of batch rows 0 .. B - 1 of one layer's cache
  * [batch_cap, seq_cap, row_bytes] (key_cache / value_cache point at the

@@ -714,3 +714,127 @@ int q3o_gqa_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, i
     parallel_for(rows ? nrows : total, nthreads, attn_range, &c);
     return 0;
 }
+
+/* ---- argmax over the last dimension: src/ops/argmax.cu:28-100 ----------- */
+
+void q3o_argmax(const uint16_t *x, int64_t rows, int64_t row_stride, int64_t search_size, int32_t *out)
+{
+    for (int64_t r = 0; r < rows; ++r)
+    {
+        float best = -INFINITY;
+        int32_t best_index = 2147483647; /* kInvalidIndex (:25) */
+        for (int64_t c = 0; c < search_size; ++c)
+        {
+            float v = FB(x[r * row_stride + c]);
+            if (v != v)
+                v = -INFINITY; /* NaN counts as -inf (:54-58) */
+            if (v > best || (v == best && (int32_t)c < best_index))
+            {
+                best = v;
+                best_index = (int32_t)c;
+            }
+        }
+        out[r] = best_index;
+    }
+}
+
+/* ---- sampling: src/generation/sampler.cpp:17-34, 134-265 ---------------- */
+
+struct q3o_cand
+{
+    double score;
+    int32_t id;
+};
+
+/* candidate_is_better (:21-27) as a qsort order: higher score first, then
+ * the smaller id */
+static int cand_order(const void *pa, const void *pb)
+{
+    const struct q3o_cand *a = (const struct q3o_cand *)pa, *b = (const struct q3o_cand *)pb;
+    if (a->score != b->score)
+        return a->score > b->score ? -1 : 1;
+    return a->id < b->id ? -1 : (a->id > b->id ? 1 : 0);
+}
+
+/* Temperature scores of row[0 .. n-1] and the reference's top-k rule: keep
+ * every candidate whose score is >= the k-th best (:160-190); returns the
+ * kept count, candidates sorted best first.  -1 for a non-finite logit. */
+static int64_t topk_sorted(const uint16_t *row, int64_t n, double temperature, int32_t top_k, struct q3o_cand *c)
+{
+    for (int64_t t = 0; t < n; ++t)
+    {
+        const float logit = FB(row[t]);
+        if (!isfinite(logit))
+            return -1;
+        c[t].score = (double)logit / temperature;
+        c[t].id = (int32_t)t;
+    }
+    qsort(c, (size_t)n, sizeof *c, cand_order);
+    int64_t kept = n;
+    if (top_k > 0 && (int64_t)top_k < n)
+    {
+        const double kth = c[top_k - 1].score;
+        kept = top_k;
+        while (kept < n && c[kept].score >= kth)
+            ++kept;
+    }
+    return kept;
+}
+
+int64_t q3o_topk_set(const uint16_t *row, int64_t n, int32_t k, int32_t *ids)
+{
+    struct q3o_cand *c = (struct q3o_cand *)malloc(sizeof *c * (size_t)n);
+    const int64_t kept = topk_sorted(row, n, 1.0, k, c);
+    for (int64_t i = 0; i < kept; ++i)
+        ids[i] = c[i].id;
+    free(c);
+    return kept;
+}
+
+int32_t q3o_sample_row(const uint16_t *row, int64_t n, float temperature, int32_t top_k, float top_p, double u)
+{
+    struct q3o_cand *c = (struct q3o_cand *)malloc(sizeof *c * (size_t)n);
+    double *w = (double *)malloc(sizeof *w * (size_t)n);
+    int32_t token = -1;
+    const int64_t kept = topk_sorted(row, n, (double)temperature, top_k, c);
+    if (kept > 0)
+    {
+        /* stable softmax (:198-215) */
+        const double maximum = c[0].score;
+        double total = 0.0;
+        for (int64_t i = 0; i < kept; ++i)
+        {
+            w[i] = exp(c[i].score - maximum);
+            total += w[i];
+        }
+        /* top-p: first prefix whose weight reaches top_p * total (:221-238) */
+        const double threshold = (double)top_p * total;
+        int64_t retained = kept;
+        double retained_weight = 0.0;
+        for (int64_t i = 0; i < kept; ++i)
+        {
+            retained_weight += w[i];
+            if (retained_weight >= threshold)
+            {
+                retained = i + 1;
+                break;
+            }
+        }
+        /* draw (:244-262) */
+        const double r = u * retained_weight;
+        double cumulative = 0.0;
+        token = c[retained - 1].id;
+        for (int64_t i = 0; i < retained; ++i)
+        {
+            cumulative += w[i];
+            if (r < cumulative)
+            {
+                token = c[i].id;
+                break;
+            }
+        }
+    }
+    free(w);
+    free(c);
+    return token;
+}

@@ -91,6 +91,22 @@ int q3o_gqa_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, i
                       const int64_t *v_strides, const int64_t *rows, int64_t nrows, uint16_t *out, uint16_t *lo,
                       uint16_t *hi, int nthreads);
 
+/* Argmax over the last dimension, src/ops/argmax.cu:28-100: per row the
+ * index of the largest of x[r * row_stride + 0 .. search_size - 1]; NaN
+ * counts as -inf, ties go to the smaller index.  Bit-exact. */
+void q3o_argmax(const uint16_t *x, int64_t rows, int64_t row_stride, int64_t search_size, int32_t *out);
+
+/* Sampling, src/generation/sampler.cpp:134-265.  q3o_topk_set: the
+ * reference's top-k set of row[0 .. n-1] (every token whose logit is >= the
+ * k-th best, ties kept; k <= 0 or >= n keeps all), ids best first (higher
+ * logit, then smaller id); returns the count, or -1 for a non-finite logit.
+ * q3o_sample_row: the whole per-row algorithm (temperature, top-k, sort,
+ * stable softmax in double, top-p, draw) given the uniform u in [0, 1) the
+ * reference takes from its mt19937_64 (:34-43); returns the token id, or -1
+ * for a non-finite logit. */
+int64_t q3o_topk_set(const uint16_t *row, int64_t n, int32_t k, int32_t *ids);
+int32_t q3o_sample_row(const uint16_t *row, int64_t n, float temperature, int32_t top_k, float top_p, double u);
+
 /* Comparison of kernel output against (primary, lo, hi).
  * stats[0] = elements, [1] = failures (outside [lo-1, hi+1]),
  * [2] = first failing index or -1, [3] = ambiguous elements (lo != hi),

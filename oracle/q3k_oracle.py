@@ -37,6 +37,9 @@ def lib() -> ctypes.CDLL:
             "q3o_kv_append": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64], None),
             "q3o_gqa_attention": ([_p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p,
                                    _int], _int),
+            "q3o_argmax": ([_p, _i64, _i64, _i64, _p], None),
+            "q3o_topk_set": ([_p, _i64, _i32, _p], _i64),
+            "q3o_sample_row": ([_p, _i64, _f32, _i32, _f32, ctypes.c_double], _i32),
             "q3o_compare_band": ([_p, _p, _p, _p, _i64, _p], None),
             "q3o_ulp_distance": ([ctypes.c_uint16, ctypes.c_uint16], ctypes.c_int32),
             "q3o_bf16_from_f32": ([_f32], ctypes.c_uint16),
@@ -185,6 +188,31 @@ def gqa_attention(q, k_cache, v_cache, Hq, start, rows=None, band=True, nthreads
         shape = (B, S, Hq * D)
         return out.reshape(shape), None if lo is None else lo.reshape(shape), None if hi is None else hi.reshape(shape)
     return out, lo, hi
+
+
+def argmax(x, search_size=0):
+    """x [..., N] bf16 bits -> int32 [...]: argmax over the first search_size (0 = all) columns."""
+    x = _a(x, np.uint16)
+    N = x.shape[-1]
+    n = search_size or N
+    rows = x.size // N
+    out = np.empty(x.shape[:-1], np.int32)
+    lib().q3o_argmax(_ptr(x), rows, N, n, _ptr(out))
+    return out
+
+
+def topk_set(row, k):
+    """The reference's top-k set of one bf16 row (ties at the k-th kept), ids best first; None if non-finite."""
+    row = _a(row, np.uint16)
+    ids = np.empty(row.size, np.int32)
+    n = lib().q3o_topk_set(_ptr(row), row.size, k, _ptr(ids))
+    return None if n < 0 else ids[:n].copy()
+
+
+def sample_row(row, temperature, top_k, top_p, u):
+    """One row of the reference sampler given its uniform draw u; -1 if non-finite."""
+    row = _a(row, np.uint16)
+    return int(lib().q3o_sample_row(_ptr(row), row.size, temperature, top_k, top_p, u))
 
 
 def compare(got, primary, lo=None, hi=None) -> dict:

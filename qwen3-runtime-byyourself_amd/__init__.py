@@ -81,6 +81,8 @@ SIGNATURES = {
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
     "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p],
+    "q3k_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p],
+    "q3k_topk_candidates_bf16": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p],
     "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "q3k_qk_norm_rope_kv_append_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p,
                                         _p, _p, _i64, _i64, _p],
@@ -190,6 +192,16 @@ def gqa_attention(q, k_cache, v_cache, out, B, S, Hq, Hkv, D, cached, start, k_s
     vs = (ctypes.c_int64 * 4)(*[int(x) for x in v_strides])
     _check(load().q3k_gqa_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), B, S, Hq, Hkv, D, cached,
                                          start, ctypes.cast(ks, _p), ctypes.cast(vs, _p), _ptr(stream)))
+
+
+def argmax(x, out, rows, row_stride, search_size, stream=None):
+    _check(load().q3k_argmax_bf16(_ptr(x), _ptr(out), rows, row_stride, search_size, _ptr(stream)))
+
+
+def topk_candidates(logits, rows, row_stride, search_size, k, cap, count, cand_index, cand_logit, nonfinite,
+                    stream=None):
+    _check(load().q3k_topk_candidates_bf16(_ptr(logits), rows, row_stride, search_size, k, cap, _ptr(count),
+                                           _ptr(cand_index), _ptr(cand_logit), _ptr(nonfinite), _ptr(stream)))
 
 
 def kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, start, stream=None):

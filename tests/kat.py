@@ -95,3 +95,19 @@ def att_inputs():
     keys = np.concatenate([hk, ck], axis=1).reshape(B, 1 + S, ATT_HKV, ATT_D)
     vals = np.concatenate([hv, cv], axis=1).reshape(B, 1 + S, ATT_HKV, ATT_D)
     return q, keys, vals
+
+
+def argmax_inputs():
+    """argmax_cuda_test.cpp:60-100: [2, 513] of -8, row 0 has 12 at 512, row 1 has 9 at 17 and at 500 (the tie
+    resolves to the smaller index); expected [512, 17]."""
+    x = np.full((2, 513), bf([-8.0])[0], np.uint16)
+    x[0, 512] = bf([12.0])[0]
+    x[1, 17] = bf([9.0])[0]
+    x[1, 500] = bf([9.0])[0]
+    return x, np.array([512, 17], np.int32)
+
+
+# Sampler KAT (sampler_cuda_test.cpp:60-160): greedy / top-1 rows and the top-k 3, top-p 0.8 row
+SAMPLER_GREEDY = np.array([[-1.0, 0.0, 4.0, 2.0, -2.0], [3.0, 7.0, 7.0, 1.0, 0.0]], np.float32)
+SAMPLER_GREEDY_IDS = [2, 1]
+SAMPLER_TOPP_ROW = np.array([2.0, 2.0, 1.0, -10.0], np.float32)   # top_k 3, top_p 0.8, T 1: only ids 0 and 1

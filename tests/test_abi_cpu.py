@@ -150,3 +150,14 @@ def test_kv_and_attention_argument_errors(q3k):
     _expect(q3k.gqa_attention, ValueError, IA, None, fake, fake, fake, 1, 2, 4, 2, 8, 3, 1, st, st)
     _expect(q3k.gqa_attention, OverflowError, OV, fake, fake, fake, fake, 2**20, 2**10, 4, 2, 8, 2**10, 0, st, st)
     q3k.gqa_attention(None, None, None, None, 0, 2, 4, 2, 8, 3, 1, st, st)
+
+
+def test_argmax_argument_errors(q3k):
+    IA = q3k.Q3K_ERR_INVALID_ARGUMENT
+    fake = 256
+    _expect(q3k.argmax, ValueError, IA, fake, fake, 2, 0, 0)
+    _expect(q3k.argmax, ValueError, IA, fake, fake, 2, 2**31, 2**31)
+    msg = _expect(q3k.argmax, ValueError, IA, fake, fake, 2, 100, 101)
+    assert "valid reduction size" in msg
+    _expect(q3k.argmax, ValueError, IA, None, fake, 2, 100, 100)
+    q3k.argmax(None, None, 0, 100, 100)

@@ -553,3 +553,75 @@ def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, n
     prim, lo, hi = oracle.gqa_attention(q, store_k, store_v, Hq, 0, rows=rows)
     check_band(oracle, name, got.reshape(-1, D)[rows], prim, lo, hi)
     assert np.isfinite(synth.bf16_to_f32(got)).all()
+
+
+# ---------------------------------------------------------------- argmax
+
+@pytest.mark.parametrize("rows,N,search,offset", [(2, 513, 0, 0), (37, 1000, 0, 0), (64, 151936, 0, 0),
+                                                  (1, 151936, 151669, 0), (5, 1003, 0, 2), (3, 4096, 77, 2),
+                                                  (700, 64, 0, 0)])
+def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset):
+    """argmax_last_dimension (argmax.cu:34-100): bit-exact indices, including NaN rows, ties, +-0, +-inf and a
+    valid-vocabulary prefix of padded logits."""
+    name = f"argmax rows={rows} N={N} search={search} offset={offset}"
+    announce(name)
+    if (rows, N) == (2, 513):
+        x, _ = kat.argmax_inputs()
+    else:
+        x = synth.normal_bf16(171, N, (rows, N), std=4.0)
+        if rows > 6:
+            x[1, :] = 0xff80
+            x[2, N // 3] = 0x7fc0
+            x[3, :] = 0x8000
+            x[3, N - 1] = 0
+            x[4, 5] = x[4, N - 2] = 0x7f80
+            x[5, :] = 0x7fc0
+            x[6, 9] = x[6, 3] = synth.f32_to_bf16(np.array([50.0], np.float32))[0]
+    X = Guarded(hip, x, offset=offset)
+    O = Guarded(hip, nbytes=rows * 4)
+    q3k.argmax(X, O, rows, N, search or N)
+    hip.synchronize()
+    assert X.guards_intact() and O.guards_intact()
+    check_exact(name, O.get(np.int32, (rows,)).view(np.uint32), oracle.argmax(x, search).view(np.uint32))
+
+
+# ---------------------------------------------------------------- sampling: top-k candidates
+
+@pytest.mark.parametrize("rows,N,valid,k", [(8, 151936, 0, 20), (4, 151936, 151669, 1), (2, 151936, 0, 1024),
+                                           (3, 5000, 0, 64), (2, 513, 500, 3)])
+def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k):
+    """GPU top-k selection (the reference sampler's top-k rule, sampler.cpp:160-190): the candidate set equals the
+    oracle's exactly, ties at the k-th included; non-finite rows flagged."""
+    name = f"topk_candidates rows={rows} N={N} valid={valid} k={k}"
+    announce(name)
+    cap = 1024
+    n = valid or N
+    x = synth.normal_bf16(174, N, (rows, N), std=3.0)
+    x[0, 5] = x[0, 9] = x[0, 200] = x[0, 3]                     # ties
+    x[0, 3] = synth.f32_to_bf16(np.array([40.0], np.float32))[0]
+    if rows > 2:
+        x[2, :] = synth.f32_to_bf16(np.array([1.5], np.float32))[0]   # all tied: count = n (> cap for large n)
+        x[2, 0] = 0x8000
+        x[2, 1] = 0x0000
+    if rows > 3:
+        x[3, n - 1] = 0x7f80                                     # non-finite inside the valid prefix
+        x[3, N - 1] = 0x7fc0 if n < N else x[3, N - 1]
+    X = Guarded(hip, x)
+    C, F = Guarded(hip, nbytes=rows * 4), Guarded(hip, nbytes=rows * 4)
+    I, V = Guarded(hip, nbytes=rows * cap * 4), Guarded(hip, nbytes=rows * cap * 2)
+    q3k.topk_candidates(X, rows, N, n, k, cap, C, I, V, F)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (X, C, F, I, V))
+    counts, flags = C.get(np.int32, (rows,)), F.get(np.int32, (rows,))
+    ids, vals = I.get(np.int32, (rows, cap)), V.get(np.uint16, (rows, cap))
+    for r in range(rows):
+        want = oracle.topk_set(x[r, :n], k)
+        if want is None:
+            assert flags[r] != 0, f"row {r}: non-finite not flagged"
+            continue
+        assert flags[r] == 0
+        assert counts[r] == want.size, (r, counts[r], want.size)
+        if want.size <= cap:
+            got = ids[r, :want.size]
+            check_exact(f"{name} row {r} ids", np.sort(got), np.sort(want))
+            check_exact(f"{name} row {r} logits", vals[r, :want.size], x[r, got])

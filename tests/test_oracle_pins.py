@@ -493,3 +493,85 @@ def test_attention_row_subset_and_planted_mistake(oracle, synth):
             out[s, h] = (w / w.sum()) @ f(vc[0, :s + 1, g])
     wrong = synth.f32_to_bf16(out.astype(np.float32)).reshape(B, S, Hq * D)
     assert oracle.compare(wrong, full, lo, hi)["fail"] > 0
+
+
+# ---------------------------------------------------------------- argmax
+
+def test_argmax_kat(oracle):
+    x, want = kat.argmax_inputs()
+    assert np.array_equal(oracle.argmax(x), want)
+
+
+def test_argmax_matches_numpy_and_edge_cases(oracle, synth):
+    """numpy's argmax returns the first maximum, as the reference's tie rule; NaN must first become -inf (numpy would
+    return the NaN's index).  Also: +0 and -0 compare equal, all -inf gives 0, the valid-size prefix."""
+    x = synth.normal_bf16(170, 1, (37, 1000), std=3.0)
+    x[3, 100] = 0x7fc0                      # NaN ignored
+    x[4, :] = 0xff80                        # all -inf -> 0
+    x[5, :] = 0x8000                        # -0 everywhere ...
+    x[5, 7] = 0x0000                        # ... and one +0: equal, the first index wins
+    x[6, 10] = x[6, 20] = 0x7f80            # two +inf: the first
+    f = synth.bf16_to_f32(x).astype(np.float64)
+    f[np.isnan(f)] = -np.inf
+    assert np.array_equal(oracle.argmax(x), np.argmax(f, axis=1).astype(np.int32))
+    assert oracle.argmax(x)[5] == 0 and oracle.argmax(x)[4] == 0 and oracle.argmax(x)[6] == 10
+    assert np.array_equal(oracle.argmax(x, 500), np.argmax(f[:, :500], axis=1).astype(np.int32))
+
+
+# ---------------------------------------------------------------- sampling
+
+def test_mt19937_64_check_value():
+    """[rand.predef]: the 10000th output of a default-constructed mt19937_64 is 9981545732273789042."""
+    from mt64 import MT19937_64
+    g = MT19937_64()
+    for _ in range(9999):
+        g()
+    assert g() == 9981545732273789042
+
+
+def test_sampler_kat(oracle):
+    """sampler_cuda_test.cpp:100-175: top_k = 1 with seed 122 gives [2, 1] (row 1 ties 7 and 7: top-k keeps both,
+    and the seed's second draw picks the smaller id); top_k 3 / top_p 0.8 only ever draws ids 0 or 1."""
+    from mt64 import MT19937_64
+    rows = kat.bf(kat.SAMPLER_GREEDY)
+    g = MT19937_64(122)
+    assert [oracle.sample_row(rows[i], 0.6, 1, 1.0, g.uniform()) for i in range(2)] == kat.SAMPLER_GREEDY_IDS
+    assert oracle.sample_row(rows[0], 0.6, 1, 1.0, 0.99) == 2                 # a unique maximum ignores the draw
+    g = MT19937_64(42)
+    for _ in range(16):
+        assert oracle.sample_row(kat.bf(kat.SAMPLER_TOPP_ROW), 1.0, 3, 0.8, g.uniform()) in (0, 1)
+    # the top-p cut: weights 1, 1, e^-1 (total 2.368); 0.8 * total is reached after two tokens
+    assert oracle.sample_row(kat.bf(kat.SAMPLER_TOPP_ROW), 1.0, 3, 0.8, 0.49) == 0
+    assert oracle.sample_row(kat.bf(kat.SAMPLER_TOPP_ROW), 1.0, 3, 0.8, 0.51) == 1
+    assert oracle.sample_row(kat.bf(np.array([1.0, np.inf], np.float32)), 1.0, 0, 1.0, 0.5) == -1
+
+
+def test_sampler_inverse_cdf_closed_form(oracle, synth):
+    """Without top-k / top-p the draw is the inverse CDF of softmax(logit / T) over tokens ordered by (score desc,
+    id asc): recomputed with numpy's lexsort and cumsum."""
+    row = synth.normal_bf16(172, 1, (1000,), std=2.0)
+    row[10] = row[20]                                            # a tie in score
+    T = 0.7
+    s = synth.bf16_to_f32(row).astype(np.float64) / np.float64(np.float32(T))
+    order = np.lexsort((np.arange(s.size), -s))
+    w = np.exp(s[order] - s[order[0]])
+    cdf = np.cumsum(w) / w.sum()
+    for u in np.random.default_rng(3).random(300):
+        want = order[min(np.searchsorted(cdf, u, side="right"), s.size - 1)]
+        assert oracle.sample_row(row, T, 0, 1.0, float(u)) == want
+    # top-k: the draw never leaves the k best (ties at the k-th included)
+    top = set(oracle.topk_set(row, 50).tolist())
+    assert all(oracle.sample_row(row, T, 50, 0.9, float(u)) in top for u in np.linspace(0, 0.999, 50))
+
+
+def test_topk_set_keeps_ties(oracle, synth):
+    row = synth.normal_bf16(173, 1, (5000,))
+    f = synth.bf16_to_f32(row)
+    for k in (1, 7, 64, 4999, 5000):
+        kth = np.sort(f)[::-1][k - 1]
+        want = np.flatnonzero(f >= kth)
+        got = oracle.topk_set(row, k)
+        assert np.array_equal(np.sort(got), want) and got.size >= k
+    tied = np.full(100, kat.bf([1.0])[0], np.uint16)
+    tied[:10] = kat.bf([3.0])[0]
+    assert oracle.topk_set(tied, 12).size == 100                  # the 12th ties with 89 others: all kept
