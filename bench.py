@@ -223,6 +223,28 @@ def time_attention(q3k, hip, synth, c, stream):
     return out
 
 
+def time_sampling(q3k, hip, synth, configs, c, stream):
+    """Next-token selection over [64, 151936] bf16 logits (a batched decode step): greedy argmax
+    (argmax.cu:34-100) and the GPU top-k candidate selection of sampling (top_k 20), both HBM bound."""
+    out = {}
+    print("[bench] timing argmax / top-k", file=sys.stderr, flush=True)
+    B, V, cap = 64, configs.VOCAB, 1024
+    x = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 43, (B, V), std=3.0))
+    ids = hip.DeviceBuffer(B * 4)
+    cnt, bad = hip.DeviceBuffer(B * 4), hip.DeviceBuffer(B * 4)
+    ci, cv = hip.DeviceBuffer(B * cap * 4), hip.DeviceBuffer(B * cap * 2)
+    ms_a = time_chain(hip, stream, [0], lambda _: [("argmax", lambda: q3k.argmax(x, ids, B, V, V, stream))], 50, 5)
+    ms_k = time_chain(hip, stream, [0], lambda _: [
+        ("topk", lambda: q3k.topk_candidates(x, B, V, V, 20, cap, cnt, ci, cv, bad, stream))], 50, 5)
+    nb = B * V * 2
+    out["argmax_b64_v151936"] = {"ms": round(ms_a, 5), "bytes": nb, "GB/s": round(nb / (ms_a * 1e-3) / 1e9, 1)}
+    out["topk20_candidates_b64_v151936"] = {"ms": round(ms_k, 5), "bytes_read_3_passes": 3 * nb,
+                                            "logits_GB/s": round(nb / (ms_k * 1e-3) / 1e9, 1)}
+    for buf in (x, ids, cnt, bad, ci, cv):
+        buf.free()
+    return out
+
+
 def read_traffic(kernel_key):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
     path = os.path.join(REPO, "profiles", "pmc_traffic_c4.md")
@@ -406,6 +428,7 @@ def main():
             for buf in e.values():
                 buf.free()
         extras.update(time_attention(q3k, hip, synth, c, stream))
+        extras.update(time_sampling(q3k, hip, synth, configs, c, stream))
         if "embedding" in c.ops:
             print("[bench] timing embedding", file=sys.stderr, flush=True)
             for s in sets[1:]:

@@ -45,7 +45,26 @@ namespace q3k
                 {
                     const int64_t nvec = n / 8;
                     const Vec8 *rv = reinterpret_cast<const Vec8 *>(r);
-                    for (int64_t i = threadIdx.x; i < nvec; i += kArgmaxBlock)
+                    // four independent 16-byte loads in flight per thread
+                    constexpr int U = 4;
+                    int64_t i = threadIdx.x;
+                    for (; i + (U - 1) * kArgmaxBlock < nvec; i += U * kArgmaxBlock)
+                    {
+                        Vec8 v[U];
+#pragma unroll
+                        for (int u = 0; u < U; ++u)
+                            v[u] = rv[i + u * kArgmaxBlock];
+#pragma unroll
+                        for (int u = 0; u < U; ++u)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                            {
+                                const uint32_t idx = static_cast<uint32_t>(8 * (i + u * kArgmaxBlock) + 2 * j);
+                                best = max_u64(best, argmax_key(v[u].d[j] & 0xffffu, idx));
+                                best = max_u64(best, argmax_key(v[u].d[j] >> 16, idx + 1));
+                            }
+                    }
+                    for (; i < nvec; i += kArgmaxBlock)
                     {
                         const Vec8 v = rv[i];
 #pragma unroll

@@ -9,8 +9,11 @@
 // or above it (index and bf16 bits, any order), so the host finishes the
 // reference's steps on about k candidates instead of V logits.
 //
-// One block of 1024 threads per row (rows strided over the grid).  A row
-// with a non-finite logit is flagged (the reference throws for it).
+// One block of 1024 threads per row (rows strided over the grid).  Logits of
+// a row share few exponents, so most increments hit a handful of bins: each
+// wave counts into its own histogram and the 16 are summed before the bin
+// search.  A row with a non-finite logit is flagged (the reference throws
+// for it).
 #include "q3k_common.hpp"
 
 namespace q3k
@@ -45,6 +48,8 @@ namespace q3k
             *rank_out = k - above;
         }
 
+        constexpr int kSelWaves = kSelBlock / kWave;
+
         __global__ __launch_bounds__(kSelBlock) void topk_select_kernel(const uint16_t *__restrict__ x, int64_t rows,
                                                                         int64_t stride, int64_t n, uint32_t k,
                                                                         int32_t cap, int32_t *__restrict__ count,
@@ -52,15 +57,31 @@ namespace q3k
                                                                         uint16_t *__restrict__ cand_logit,
                                                                         int32_t *__restrict__ nonfinite)
         {
+            __shared__ uint32_t wave_hist[kSelWaves][256];
             __shared__ uint32_t hist[256];
             __shared__ uint32_t sel[2];
             __shared__ uint32_t found, bad;
             const int tid = threadIdx.x;
+            const int wave = tid / kWave;
+            uint32_t *my_hist = wave_hist[wave];
+            auto clear = [&]() {
+                for (int i = tid; i < kSelWaves * 256; i += kSelBlock)
+                    (&wave_hist[0][0])[i] = 0u;
+            };
+            auto merge = [&]() {
+                if (tid < 256)
+                {
+                    uint32_t sum = 0u;
+#pragma unroll
+                    for (int w = 0; w < kSelWaves; ++w)
+                        sum += wave_hist[w][tid];
+                    hist[tid] = sum;
+                }
+            };
             for (int64_t row = blockIdx.x; row < rows; row += gridDim.x)
             {
                 const uint16_t *r = x + row * stride;
-                if (tid < 256)
-                    hist[tid] = 0u;
+                clear();
                 if (tid == 0)
                 {
                     found = 0u;
@@ -72,25 +93,26 @@ namespace q3k
                 {
                     const uint32_t b = r[c];
                     my_bad |= (b & 0x7f80u) == 0x7f80u ? 1u : 0u;
-                    atomicAdd(&hist[sel_key(b) >> 8], 1u);
+                    atomicAdd(&my_hist[sel_key(b) >> 8], 1u);
                 }
                 if (my_bad)
                     atomicOr(&bad, 1u);
                 __syncthreads();
+                merge();
+                __syncthreads();
                 if (tid == 0)
                     find_bin(hist, k, &sel[0], &sel[1]);
+                clear();
                 __syncthreads();
                 const uint32_t hi = sel[0], rank = sel[1];
-                __syncthreads();
-                if (tid < 256)
-                    hist[tid] = 0u;
-                __syncthreads();
                 for (int64_t c = tid; c < n; c += kSelBlock)
                 {
                     const uint32_t key = sel_key(r[c]);
                     if ((key >> 8) == hi)
-                        atomicAdd(&hist[key & 255u], 1u);
+                        atomicAdd(&my_hist[key & 255u], 1u);
                 }
+                __syncthreads();
+                merge();
                 __syncthreads();
                 if (tid == 0)
                 {
