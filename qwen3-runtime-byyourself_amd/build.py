@@ -28,7 +28,7 @@ INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 OBJ_DIR = os.path.join(PKG_DIR, "build")
 KERNEL_DIR = os.path.join(PKG_DIR, "csrc", "kernels")
-HOST_DIRS = [os.path.join(PKG_DIR, "csrc", d) for d in ("core", "ops", "model", "generation")]
+HOST_DIRS = [os.path.join(PKG_DIR, "csrc", d) for d in ("core", "ops", "model", "generation", "io")]
 ORACLE_DIR = os.path.join(REPO_DIR, "oracle")
 CPP_TEST_DIR = os.path.join(REPO_DIR, "tests", "cpp")
 

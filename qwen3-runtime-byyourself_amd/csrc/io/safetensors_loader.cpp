@@ -1,0 +1,157 @@
+// Tensor loading from one safetensors file (behaviour of the reference's
+// src/io/safetensors_loader.cpp).  load(): one tensor, plain copy.
+// load_many() to a GPU: chunks of at most 32 MiB are copied from the mapped
+// file into one of two pinned staging buffers and sent with an async
+// host-to-device copy on the loader's non-blocking stream; a buffer is
+// refilled once the event of its previous copy has completed, so the host
+// copy of chunk i + 1 overlaps the DMA of chunk i.
+#include "qwen3/io/safetensors_loader.h"
+
+#include "qwen3/hip/hip_check.h"
+
+#include <algorithm>
+#include <cstring>
+#include <stdexcept>
+
+namespace qwen3
+{
+    SafetensorsLoader::SafetensorsLoader(const std::filesystem::path &model_path) : file_(model_path), metadata_(file_)
+    {
+    }
+
+    SafetensorsLoader::~SafetensorsLoader() { release_transfer_resources(); }
+
+    const std::byte *SafetensorsLoader::source_data(const SafetensorsTensorInfo &info) const noexcept
+    {
+        return file_.data_bytes().data() + info.begin_offset;
+    }
+
+    Tensor SafetensorsLoader::load(std::string_view tensor_name, Device target_device) const
+    {
+        const SafetensorsTensorInfo &info = metadata_.tensor(tensor_name);
+        Tensor result = Tensor::empty(info.shape, info.dtype, target_device);
+        if (result.nbytes() != info.size_bytes())
+            throw std::logic_error("Tensor size does not match metadata for '" + std::string(tensor_name) + "'");
+        if (info.size_bytes() == 0)
+            return result;
+        if (target_device.is_cpu())
+        {
+            std::memcpy(result.data(), source_data(info), info.size_bytes());
+            return result;
+        }
+        hip::DeviceGuard guard(target_device.index());
+        QWEN3_HIP_CHECK(hipMemcpy(result.data(), source_data(info), info.size_bytes(), hipMemcpyHostToDevice));
+        return result;
+    }
+
+    void SafetensorsLoader::ensure_transfer_resources(int device_index)
+    {
+        if (stream_ != nullptr && transfer_device_ == device_index)
+            return;
+        release_transfer_resources();
+        transfer_device_ = device_index;
+        try
+        {
+            QWEN3_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+            for (std::size_t i = 0; i < kStagingSlotCount; ++i)
+            {
+                QWEN3_HIP_CHECK(hipHostMalloc(&staging_[i], kStagingBufferBytes, hipHostMallocDefault));
+                QWEN3_HIP_CHECK(hipEventCreateWithFlags(&events_[i], hipEventDisableTiming));
+            }
+        }
+        catch (...)
+        {
+            release_transfer_resources();
+            throw;
+        }
+    }
+
+    void SafetensorsLoader::release_transfer_resources() noexcept
+    {
+        if (transfer_device_ < 0)
+            return;
+        int previous = 0;
+        const bool restore = hipGetDevice(&previous) == hipSuccess;
+        (void)hipSetDevice(transfer_device_);
+        if (stream_ != nullptr)
+            (void)hipStreamSynchronize(stream_);
+        for (auto &e : events_)
+            if (e != nullptr)
+            {
+                (void)hipEventDestroy(e);
+                e = nullptr;
+            }
+        for (auto &b : staging_)
+            if (b != nullptr)
+            {
+                (void)hipHostFree(b);
+                b = nullptr;
+            }
+        if (stream_ != nullptr)
+        {
+            (void)hipStreamDestroy(stream_);
+            stream_ = nullptr;
+        }
+        transfer_device_ = -1;
+        if (restore)
+            (void)hipSetDevice(previous);
+    }
+
+    std::vector<Tensor> SafetensorsLoader::load_many(const std::vector<std::string> &tensor_names, Device target_device)
+    {
+        std::vector<Tensor> results;
+        results.reserve(tensor_names.size());
+        if (tensor_names.empty())
+            return results;
+        if (target_device.is_cpu())
+        {
+            for (const std::string &name : tensor_names)
+                results.push_back(load(name, target_device));
+            return results;
+        }
+        if (!target_device.is_cuda())
+            throw std::invalid_argument("unsupported target device");
+        hip::DeviceGuard guard(target_device.index());
+        ensure_transfer_resources(target_device.index());
+        std::vector<const SafetensorsTensorInfo *> infos;
+        infos.reserve(tensor_names.size());
+        for (const std::string &name : tensor_names)
+        {
+            const SafetensorsTensorInfo &info = metadata_.tensor(name);
+            infos.push_back(&info);
+            results.push_back(Tensor::empty(info.shape, info.dtype, target_device));
+            if (results.back().nbytes() != info.size_bytes())
+                throw std::logic_error("Tensor size does not match metadata for '" + name + "'");
+        }
+        std::array<bool, kStagingSlotCount> in_flight{{false, false}};
+        std::size_t next = 0;
+        try
+        {
+            for (std::size_t t = 0; t < results.size(); ++t)
+            {
+                const SafetensorsTensorInfo &info = *infos[t];
+                const std::byte *src = source_data(info);
+                auto *dst = static_cast<std::byte *>(results[t].data());
+                for (std::size_t done = 0; done < info.size_bytes();)
+                {
+                    const std::size_t slot = next++ % kStagingSlotCount;
+                    if (in_flight[slot])
+                        QWEN3_HIP_CHECK(hipEventSynchronize(events_[slot]));
+                    const std::size_t chunk = std::min(info.size_bytes() - done, kStagingBufferBytes);
+                    std::memcpy(staging_[slot], src + done, chunk);
+                    QWEN3_HIP_CHECK(hipMemcpyAsync(dst + done, staging_[slot], chunk, hipMemcpyHostToDevice, stream_));
+                    QWEN3_HIP_CHECK(hipEventRecord(events_[slot], stream_));
+                    in_flight[slot] = true;
+                    done += chunk;
+                }
+            }
+            QWEN3_HIP_CHECK(hipStreamSynchronize(stream_));
+        }
+        catch (...)
+        {
+            (void)hipStreamSynchronize(stream_);
+            throw;
+        }
+        return results;
+    }
+} // namespace qwen3

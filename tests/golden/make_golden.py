@@ -7,6 +7,12 @@ here (CUDA, and its src/core is missing), so these vectors record the
 oracle's outputs after it was pinned by tests/test_oracle_pins.py; they guard
 the oracle (and, through the GPU tests, the kernels) against drift.
 
+The safetensors fixtures (safetensors_single/, safetensors_sharded/) are
+written by the official `safetensors` package (torch writer) so that the C++
+reader is checked against files it did not produce: BF16 / F32 / I32 tensors
+with arange-based values (bf16 value i = (i % 251) - 125 as float, exact),
+__metadata__, and a two-shard checkpoint with its index.
+
 Run from the repository root: python tests/golden/make_golden.py
 """
 import importlib
@@ -60,7 +66,41 @@ def fixtures(oracle):
     return out
 
 
+def safetensors_fixtures():
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    def bf(n):
+        return ((torch.arange(n) % 251) - 125).to(torch.bfloat16)
+
+    single = os.path.join(HERE, "safetensors_single")
+    os.makedirs(single, exist_ok=True)
+    tensors = {
+        "model.embed_tokens.weight": bf(6 * 8).reshape(6, 8),
+        "model.norm.weight": bf(8),
+        "rope.inv_freq": torch.arange(4, dtype=torch.float32) * 0.25,
+        "positions": torch.arange(5, dtype=torch.int32) - 2,
+    }
+    save_file(tensors, os.path.join(single, "model.safetensors"), metadata={"format": "pt"})
+    sharded = os.path.join(HERE, "safetensors_sharded")
+    os.makedirs(sharded, exist_ok=True)
+    shard_a = {"a.weight": bf(3 * 4).reshape(3, 4), "a.bias": bf(4)}
+    shard_b = {"b.weight": bf(2 * 16).reshape(2, 16), "b.scale": torch.ones(3, dtype=torch.float32)}
+    names = ["model-00001-of-00002.safetensors", "model-00002-of-00002.safetensors"]
+    save_file(shard_a, os.path.join(sharded, names[0]), metadata={"format": "pt"})
+    save_file(shard_b, os.path.join(sharded, names[1]), metadata={"format": "pt"})
+    total = sum(t.numel() * t.element_size() for t in list(shard_a.values()) + list(shard_b.values()))
+    index = {"metadata": {"total_size": total},
+             "weight_map": {**{k: names[0] for k in shard_a}, **{k: names[1] for k in shard_b}}}
+    with open(os.path.join(sharded, "model.safetensors.index.json"), "w") as f:
+        json.dump(index, f, indent=2, sort_keys=True)
+    print("wrote safetensors fixtures")
+
+
 def main():
+    safetensors_fixtures()
     oracle = load_oracle()
     for name, arrays in fixtures(oracle).items():
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **arrays)
