@@ -199,16 +199,19 @@ def time_attention(q3k, hip, synth, c, stream):
     at 64 sequences x 4096 cached keys (HBM bound: the K/V cache is read once)."""
     out = {}
     print("[bench] timing attention", file=sys.stderr, flush=True)
-    for name, B, S, start in (("prefill", c.batch, c.seq, 0), ("decode_b64_l4096", 64, 1, 4095)):
+    for name, B, S, start in (("prefill", c.batch, c.seq, 0), ("decode_b64_l4096", 64, 1, 4095),
+                              ("decode_b1_l4096", 1, 1, 4095)):
         L = start + S
         q = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 40, (B, S, c.heads_q * D)))
         kc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 41, (B, L, c.heads_kv, D)))
         vc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 42, (B, L, c.heads_kv, D)))
         o = hip.DeviceBuffer(B * S * c.heads_q * D * 2)
         st = (L * c.heads_kv * D, c.heads_kv * D, D, 1)
+        wb = q3k.gqa_attention_workspace_bytes(B, S, c.heads_q, c.heads_kv, D, L)
+        ws = hip.DeviceBuffer(wb) if wb else None   # a launch too small for the GPU splits the key range
         ms = time_chain(hip, stream, [0], lambda _: [
             ("attention", lambda: q3k.gqa_attention(q, kc, vc, o, B, S, c.heads_q, c.heads_kv, D, L, start, st, st,
-                                                    stream))], 10 if S > 1 else 50, 2)
+                                                    stream, workspace=ws, workspace_bytes=wb))], 10 if S > 1 else 50, 2)
         flops = attention_flops(B, S, start, c.heads_q, D)
         byts = 2 * B * L * c.heads_kv * D * 2 + 2 * B * S * c.heads_q * D * 2
         rec = {"ms": round(ms, 5), "B": B, "S": S, "cached": L, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
@@ -217,8 +220,9 @@ def time_attention(q3k, hip, synth, c, stream):
             rec["pct_of_bf16_peak"] = round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
         else:
             rec["pct_of_hbm_peak"] = round(100 * byts / (ms * 1e-3) / 1e9 / PEAK_GBS, 2)
+        rec["key_splits"] = wb > 0
         out["attention_" + name] = rec
-        for buf in (q, kc, vc, o):
+        for buf in (q, kc, vc, o) + ((ws,) if ws else ()):
             buf.free()
     return out
 

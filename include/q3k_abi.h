@@ -177,7 +177,12 @@ Q3K_API int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k,
  * h / (Hq / Hkv); scale 1 / sqrt(D).  cached must equal start + S.
  * out [B, S, Hq * D] bf16.  head_dim 128 with unit dim stride and 16-byte
  * aligned rows takes the matrix-core kernel, anything up to 256 the generic
- * one.  Replaces qwen3::ops::grouped_query_attention,
+ * one.  workspace (16-byte aligned device memory, may be NULL) of at least
+ * q3k_gqa_attention_workspace_bytes(...) bytes lets a launch too small to
+ * fill the GPU (decode with few sequences) split the key range across
+ * blocks and merge the slices; without it the launch is not split.  Calls
+ * that share a workspace must not overlap.
+ * Replaces qwen3::ops::grouped_query_attention,
  * src/ops/gqa_attention.cu:304-345 (kernel :20-155, checks :157-302).
  */
 Q3K_API int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache,
@@ -185,7 +190,16 @@ Q3K_API int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache,
                           int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
                           int64_t cached, int64_t start,
                           const int64_t *k_strides, const int64_t *v_strides,
+                          void *workspace, int64_t workspace_bytes,
                           q3k_stream_t stream);
+
+/*
+ * Workspace bytes q3k_gqa_attention_bf16 would use to split this shape's
+ * key range (0: it does not split).  No counterpart in the reference (its
+ * kernel is one block per query row).
+ */
+Q3K_API int64_t q3k_gqa_attention_workspace_bytes(int64_t B, int64_t S,
+                          int32_t Hq, int32_t Hkv, int32_t D, int64_t cached);
 
 /*
  * Argmax over the last dimension: out[r] = index of the largest of

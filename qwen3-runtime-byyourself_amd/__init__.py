@@ -80,7 +80,8 @@ SIGNATURES = {
     "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
-    "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p],
+    "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p, _i64, _p],
+    "q3k_gqa_attention_workspace_bytes": [_i64, _i64, _i32, _i32, _i32, _i64],
     "q3k_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p],
     "q3k_topk_candidates_bf16": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p],
     "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
@@ -116,7 +117,7 @@ def load(path: str | None = None) -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = ctypes.c_int64 if name.endswith("_bytes") else ctypes.c_int
     lib.q3k_last_error_string.restype = ctypes.c_char_p
     lib.q3k_last_error_string.argtypes = []
     lib.q3k_version.restype = ctypes.c_char_p
@@ -186,12 +187,18 @@ def qk_norm_rope(q, k, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, positions
                                         _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
 
 
-def gqa_attention(q, k_cache, v_cache, out, B, S, Hq, Hkv, D, cached, start, k_strides, v_strides, stream=None):
+def gqa_attention(q, k_cache, v_cache, out, B, S, Hq, Hkv, D, cached, start, k_strides, v_strides, stream=None,
+                  workspace=None, workspace_bytes=0):
     """k_strides / v_strides: 4 element strides (batch, position, head, dim) of the cache views."""
     ks = (ctypes.c_int64 * 4)(*[int(x) for x in k_strides])
     vs = (ctypes.c_int64 * 4)(*[int(x) for x in v_strides])
     _check(load().q3k_gqa_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), B, S, Hq, Hkv, D, cached,
-                                         start, ctypes.cast(ks, _p), ctypes.cast(vs, _p), _ptr(stream)))
+                                         start, ctypes.cast(ks, _p), ctypes.cast(vs, _p), _ptr(workspace),
+                                         workspace_bytes, _ptr(stream)))
+
+
+def gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, cached):
+    return int(load().q3k_gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, cached))
 
 
 def argmax(x, out, rows, row_stride, search_size, stream=None):

@@ -59,6 +59,15 @@ namespace q3k
             int32_t D;
             int32_t qblocks;
             float scale;
+            // split-K: the key range is cut into `splits` slices of split_keys
+            // keys (a multiple of the tile); slice results (unnormalised O^T,
+            // running max and sum) go to part_o [splits, rows, D] and part_ml
+            // [splits, rows, 2] and attn_combine_kernel merges them
+            int32_t splits;
+            int32_t split_keys;
+            float *part_o;
+            float *part_ml;
+            int64_t rows;
         };
 
         __device__ __forceinline__ bf16x8_t as_bf8(const Vec8 &v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -101,8 +110,10 @@ namespace q3k
             const int lane = threadIdx.x % kWave;
             const int li = lane % 32, lg = lane / 32;
 
-            // block -> (batch, KV head, query block); the longest query blocks go first
+            // block -> (key slice, batch, KV head, query block); the longest query blocks go first
             int bid = blockIdx.x;
+            const int sp = bid % a.splits;
+            bid /= a.splits;
             const int qb = a.qblocks - 1 - bid % a.qblocks;
             bid /= a.qblocks;
             const int kvh = bid % a.Hkv;
@@ -112,7 +123,11 @@ namespace q3k
             const int32_t s0 = qb * QP;
             const int32_t s_last = (s0 + QP < S ? s0 + QP : S) - 1;
             const int32_t n_keys = start + s_last + 1;
-            const int ntiles = (n_keys + kKeyTile - 1) / kKeyTile;
+            // this block's key slice [sp * split_keys, ...) within the causal range
+            const int32_t k_begin = sp * a.split_keys;
+            const int32_t k_end = n_keys < k_begin + a.split_keys ? n_keys : k_begin + a.split_keys;
+            const int tile_begin = k_begin / kKeyTile;
+            const int ntiles = k_end > k_begin ? (k_end + kKeyTile - 1) / kKeyTile : tile_begin;
 
             // this lane's column
             const int32_t wave_s0 = s0 + wave * PW;
@@ -184,10 +199,13 @@ namespace q3k
             float m = -__builtin_huge_valf(), l = 0.0f;
             const float scale2 = a.scale * kLog2e;
 
-            load_tile(0);
-            store_tile(lds[0]);
+            if (tile_begin < ntiles)
+            {
+                load_tile(tile_begin);
+                store_tile(lds[tile_begin % 2]);
+            }
             __syncthreads();
-            for (int tile = 0; tile < ntiles; ++tile)
+            for (int tile = tile_begin; tile < ntiles; ++tile)
             {
                 const bool more = tile + 1 < ntiles;
                 if (more)
@@ -291,6 +309,25 @@ namespace q3k
 
             if (!col_ok)
                 return;
+            if (a.splits > 1)
+            {
+                const int64_t slot = static_cast<int64_t>(sp) * a.rows + (b * S + s_col) * a.Hq + h_col;
+                float *po = a.part_o + slot * kAttD;
+#pragma unroll
+                for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4)
+                    {
+                        const float4 w = {o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+                        *reinterpret_cast<float4 *>(po + dt * 32 + 8 * q4 + 4 * lg) = w;
+                    }
+                if (lg == 0)
+                {
+                    a.part_ml[2 * slot] = m;
+                    a.part_ml[2 * slot + 1] = l;
+                }
+                return;
+            }
             const float inv = 1.0f / l;
             uint16_t *orow = a.out + ((b * S + s_col) * a.Hq + h_col) * kAttD;
 #pragma unroll
@@ -304,6 +341,36 @@ namespace q3k
                     w.y = pack_rne(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
                     *reinterpret_cast<uint2 *>(orow + d) = w;
                 }
+        }
+
+        // Merges the key slices of one query row per wave: weights
+        // 2^(m_s - max m) (the running maxima are in the log2 domain), then
+        // sum_s w_s O_s / sum_s w_s l_s; lane t holds dims 2t, 2t + 1.
+        __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__restrict__ part_o,
+                                                                      const float *__restrict__ part_ml,
+                                                                      uint16_t *__restrict__ out, int64_t rows,
+                                                                      int32_t splits)
+        {
+            const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
+                                __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+            if (row >= rows)
+                return;
+            const int lane = threadIdx.x % kWave;
+            float mx = -__builtin_huge_valf();
+            for (int sp = 0; sp < splits; ++sp)
+                mx = fmaxf(mx, part_ml[2 * (static_cast<int64_t>(sp) * rows + row)]);
+            float lsum = 0.0f, a0 = 0.0f, a1 = 0.0f;
+            for (int sp = 0; sp < splits; ++sp)
+            {
+                const int64_t slot = static_cast<int64_t>(sp) * rows + row;
+                const float w = __builtin_amdgcn_exp2f(part_ml[2 * slot] - mx);
+                lsum += w * part_ml[2 * slot + 1];
+                const float2 v = reinterpret_cast<const float2 *>(part_o + slot * kAttD)[lane];
+                a0 += w * v.x;
+                a1 += w * v.y;
+            }
+            const float inv = 1.0f / lsum;
+            reinterpret_cast<uint32_t *>(out + row * kAttD)[lane] = pack_rne(a0 * inv, a1 * inv);
         }
 
         // Generic path: one wave per query row (b, s, h); lane t holds head
@@ -374,13 +441,54 @@ namespace q3k
                    aligned16(a.k) && aligned16(a.v) && aligned_to(a.out, 8);
         }
 
+        // Below this many blocks the grid leaves CUs idle and the key range is
+        // split; a slice keeps at least two tiles.
+        constexpr int64_t kSplitTargetBlocks = 512;
+        constexpr int32_t kMinSplitKeys = 2 * kKeyTile;
+
+        struct SplitPlan
+        {
+            int32_t splits = 1;
+            int32_t split_keys = INT32_MAX;
+            int64_t bytes = 0;
+        };
+
+        SplitPlan plan_split(int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int64_t cached)
+        {
+            SplitPlan p;
+            const int32_t G = Hq / Hkv;
+            const int64_t QP = 4 * (32 / (G > 32 ? 32 : G));
+            const int64_t blocks = B * Hkv * ((S + QP - 1) / QP);
+            if (blocks >= kSplitTargetBlocks || cached < 2 * kMinSplitKeys)
+                return p;
+            int64_t want = (kSplitTargetBlocks + blocks - 1) / blocks;
+            const int64_t most = cached / kMinSplitKeys;
+            if (want > most)
+                want = most;
+            if (want > 64)
+                want = 64;
+            if (want < 2)
+                return p;
+            int64_t keys = (cached + want - 1) / want;
+            keys = (keys + kKeyTile - 1) / kKeyTile * kKeyTile;
+            p.splits = static_cast<int32_t>((cached + keys - 1) / keys);
+            p.split_keys = static_cast<int32_t>(keys);
+            if (p.splits < 2)
+                return SplitPlan{};
+            p.bytes = static_cast<int64_t>(p.splits) * B * S * Hq * (kAttD + 2) * 4;
+            return p;
+        }
+
         template <int G>
         void launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
         {
             constexpr int QP = 4 * (32 / G);
             a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
-            const int64_t blocks = B * a.Hkv * a.qblocks;
+            const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
             attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(a);
+            if (a.splits > 1)
+                attn_combine_kernel<<<dim3(static_cast<unsigned>((a.rows + 3) / 4)), dim3(kBlock), 0, stream>>>(
+                    a.part_o, a.part_ml, a.out, a.rows, a.splits);
         }
     } // namespace
 } // namespace q3k
@@ -388,7 +496,8 @@ namespace q3k
 extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                                       uint16_t *out, int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
                                       int64_t cached, int64_t start, const int64_t *k_strides,
-                                      const int64_t *v_strides, q3k_stream_t stream)
+                                      const int64_t *v_strides, void *workspace, int64_t workspace_bytes,
+                                      q3k_stream_t stream)
 {
     using namespace q3k;
     if (B < 0 || S < 0)
@@ -436,10 +545,23 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
                Hkv,
                D,
                0,
-               1.0f / __builtin_sqrtf(static_cast<float>(D))};
+               1.0f / __builtin_sqrtf(static_cast<float>(D)),
+               1,
+               INT32_MAX,
+               nullptr,
+               nullptr,
+               B * S * Hq};
     const int32_t G = Hq / Hkv;
     if (mfma_ok(a, G))
     {
+        const SplitPlan plan = plan_split(B, S, Hq, Hkv, cached);
+        if (plan.splits > 1 && workspace != nullptr && workspace_bytes >= plan.bytes && aligned16(workspace))
+        {
+            a.splits = plan.splits;
+            a.split_keys = plan.split_keys;
+            a.part_o = static_cast<float *>(workspace);
+            a.part_ml = a.part_o + static_cast<int64_t>(plan.splits) * a.rows * kAttD;
+        }
         switch (G)
         {
         case 1: launch_mfma<1>(a, B, s); break;
@@ -455,4 +577,13 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
     const int64_t blocks = (rows + (kBlock / kWave) - 1) / (kBlock / kWave);
     attn_generic_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(a, rows);
     return check_launch("grouped_query_attention (generic)");
+}
+
+extern "C" int64_t q3k_gqa_attention_workspace_bytes(int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
+                                                     int64_t cached)
+{
+    if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != q3k::kAttD || cached < S ||
+        B * S * Hq > INT32_MAX)
+        return 0;
+    return q3k::plan_split(B, S, Hq, Hkv, cached).bytes;
 }

@@ -51,13 +51,19 @@ namespace qwen3::ops
                                         key_cache.stride(3)};
             const std::int64_t vs[4] = {value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
                                         value_cache.stride(3)};
+            const std::int64_t B = query.shape()[0], S = query.shape()[1];
+            const auto Hkv = static_cast<std::int32_t>(key_cache.shape()[2]);
+            const auto D = static_cast<std::int32_t>(key_cache.shape()[3]);
+            // a launch too small for the GPU splits the key range; its slices need a workspace
+            const std::int64_t ws_bytes =
+                q3k_gqa_attention_workspace_bytes(B, S, num_query_heads, Hkv, D, key_cache.shape()[1]);
+            Tensor workspace = Tensor::empty(Shape{(ws_bytes + 3) / 4}, DType::Float32, query.device());
             detail::launch_on(query.device(), [&](q3k_stream_t stream) {
                 return q3k_gqa_attention_bf16(
                     detail::bf16_ptr(query), static_cast<const uint16_t *>(key_cache.data()),
-                    static_cast<const uint16_t *>(value_cache.data()), detail::bf16_ptr(output), query.shape()[0],
-                    query.shape()[1], num_query_heads, static_cast<std::int32_t>(key_cache.shape()[2]),
-                    static_cast<std::int32_t>(key_cache.shape()[3]), key_cache.shape()[1], start_position, ks, vs,
-                    stream);
+                    static_cast<const uint16_t *>(value_cache.data()), detail::bf16_ptr(output), B, S,
+                    num_query_heads, Hkv, D, key_cache.shape()[1], start_position, ks, vs,
+                    ws_bytes > 0 ? workspace.data() : nullptr, ws_bytes, stream);
             });
         }
     } // namespace

@@ -482,16 +482,21 @@ def test_qk_norm_rope_kv_append(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, Sc, c
 
 # ---------------------------------------------------------------- attention
 
-def run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, offset=0):
+def run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, offset=0, split=False):
     """q [B, S, Hq * D]; the caches are whole KvCache-like layers [Bcap, Scap, Hkv, D], read through the
-    [B, start + S] view (strides of the storage), as KvCache::key_view hands them over."""
+    [B, start + S] view (strides of the storage), as KvCache::key_view hands them over.  With split, a workspace of
+    the size the library asks for lets it split the key range."""
     _, Scap, Hkv, D = store_k.shape
     Q, K, V = Guarded(hip, q, offset=offset), Guarded(hip, store_k, offset=offset), Guarded(hip, store_v, offset=offset)
     O = Guarded(hip, nbytes=q.nbytes, offset=offset)
     st = (Scap * Hkv * D, Hkv * D, D, 1)
-    q3k.gqa_attention(Q, K, V, O, B, S, Hq, Hkv, D, start + S, start, st, st)
+    ws_bytes = q3k.gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, start + S) if split else 0
+    if split:
+        assert ws_bytes > 0, "this shape should split"
+    W = Guarded(hip, nbytes=ws_bytes) if ws_bytes else None
+    q3k.gqa_attention(Q, K, V, O, B, S, Hq, Hkv, D, start + S, start, st, st, workspace=W, workspace_bytes=ws_bytes)
     hip.synchronize()
-    assert all(b.guards_intact() for b in (Q, K, V, O))
+    assert all(b.guards_intact() for b in (Q, K, V, O) + ((W,) if W else ()))
     assert np.array_equal(Q.get(np.uint16, q.shape), q) and np.array_equal(K.get(np.uint16, store_k.shape), store_k)
     return O.get(np.uint16, q.shape)
 
@@ -625,3 +630,22 @@ def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k):
             got = ids[r, :want.size]
             check_exact(f"{name} row {r} ids", np.sort(got), np.sort(want))
             check_exact(f"{name} row {r} logits", vals[r, :want.size], x[r, got])
+
+
+@pytest.mark.parametrize("B,S,start,Hq,Hkv,cap", [(1, 1, 4095, 32, 8, 4096), (2, 5, 700, 32, 8, 800),
+                                                 (1, 1, 300, 64, 8, 320), (1, 3, 400, 16, 8, 420),
+                                                 (4, 1, 1000, 32, 8, 1100)])
+def test_gqa_attention_split_keys(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, cap):
+    """Decode with few sequences: the key range is split across blocks (the workspace the library asks for) and the
+    slices merged; same band as the single-pass kernel."""
+    D = 128
+    name = f"gqa_attention split B={B} S={S} start={start} Hq={Hq} Hkv={Hkv}"
+    announce(name)
+    q = synth.normal_bf16(166, S, (B, S, Hq * D))
+    store_k = synth.normal_bf16(167, S, (B, cap, Hkv, D))
+    store_v = synth.normal_bf16(168, S, (B, cap, Hkv, D))
+    got = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, split=True)
+    prim, lo, hi = oracle.gqa_attention(q, store_k[:, :start + S], store_v[:, :start + S], Hq, start)
+    check_band(oracle, name, got, prim, lo, hi)
+    whole = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start)
+    check_band(oracle, name + " (not split)", whole, prim, lo, hi)
