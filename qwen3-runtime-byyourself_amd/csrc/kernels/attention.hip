@@ -12,16 +12,20 @@
 //   online softmax per column: a lane holds one column, so the key max and
 //                 sum need only its own registers and the lane 32 apart
 //                 (v_permlane32_swap);
-//   O^T += V^T P^T: A = V^T from a transposed LDS copy of the tile, B = P^T
-//                 straight from the S^T registers.  P is split into a bf16
-//                 high part and a bf16 remainder (two MFMAs), so the weights
-//                 keep about 16 significant bits: the reference accumulates
-//                 p * v in fp32, and a single bf16 rounding of p would cost
-//                 up to half an output ulp.
+//   O^T += V^T P^T: A = V^T read from the row-major V tile with the LDS
+//                 transpose read (ds_read_b64_tr_b16), B = P^T straight from
+//                 the S^T registers.  P is split into a bf16 high part and a
+//                 bf16 remainder (two MFMAs), so the weights keep about 16
+//                 significant bits: the reference accumulates p * v in fp32,
+//                 and a single bf16 rounding of p would cost up to half an
+//                 output ulp.
 // Scores are scaled by scale * log2(e) and exponentiated with v_exp_f32.
-// Keys go in tiles of 64 (two S^T halves of 32): a tile's K and V are loaded
-// into registers while the previous tile is computed, then stored to the
-// other of two LDS buffers, one barrier per tile.
+// Keys go in tiles of 64 (two S^T halves of 32).  A tile's K and V rows go
+// from HBM straight into LDS (global_load_lds_dwordx4, no registers) while
+// the previous tile is computed, into the other of two buffers; one barrier
+// per tile.  Tile rows are 256 bytes with the 16-byte chunks XOR-swizzled by
+// row so that the K fragment reads (ds_read_b128) and the V transpose reads
+// hit distinct LDS banks.
 //
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
 // keys in order, lanes over the head dimension -- the reference's own
@@ -35,13 +39,16 @@ namespace q3k
         typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
         typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+        typedef __attribute__((address_space(3))) void lds_void_t;
+
         constexpr int kAttD = 128;
-        constexpr int kKeyTile = 64;                   // keys per pipeline step
-        constexpr int kKRowBytes = kAttD * 2 + 16;     // K tile row in LDS, padded: conflict-free b128 reads
-        constexpr int kVtRowBytes = kKeyTile * 2 + 16; // V^T tile row (one head-dim index), padded likewise
-        constexpr int kKTileBytes = kKeyTile * kKRowBytes;
-        constexpr int kVtTileBytes = kAttD * kVtRowBytes;
-        constexpr int kTileBytes = kKTileBytes + kVtTileBytes;
+        constexpr int kKeyTile = 64;                          // keys per pipeline step
+        constexpr int kRowBytes = kAttD * 2;                  // one K or V row in LDS
+        constexpr int kHalfBytes = kKeyTile * kRowBytes;      // the K (or V) rows of a tile
+        constexpr int kTileBytes = 2 * kHalfBytes;            // K rows, then V rows
+        constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
         constexpr float kLog2e = 1.4426950408889634f;
 
         struct AttnArgs
@@ -72,16 +79,18 @@ namespace q3k
 
         __device__ __forceinline__ bf16x8_t as_bf8(const Vec8 &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-        // LDS position of key kk (0..63) in a V^T row.  Within each half of 32
-        // keys, bits 2 and 3 are swapped, so that the 8 keys lane group g feeds
-        // to the PV MFMA of chunk m (keys 16m + 8h + 4g + j, h < 2, j < 4: the
-        // S^T accumulator rows the lane holds) are 8 consecutive positions.
-        __device__ __forceinline__ int vt_pos(int kk) { return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1); }
+        // LDS chunk (16 bytes) holding chunk c of K row r / V row r of a tile.
+        // K: lanes 0..31 of a fragment read read rows r..r+31 at one chunk;
+        // any 16 consecutive rows put it in 16 different chunk positions.
+        // V: a transpose read takes 4 rows x 32 bytes per 16 lanes; rows
+        // 4 apart share a bank set.
+        __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
+        __device__ __forceinline__ int v_slot(int r, int c) { return c ^ (4 * (r & 3)); }
 
-        __device__ __forceinline__ uint32_t bf_pair(uint32_t lo_word, uint32_t hi_word, int half)
+        // 16 bytes per lane from global memory into LDS at lds_wave + 16 * lane
+        __device__ __forceinline__ void dma16(const void *src, unsigned char *lds_wave)
         {
-            // element `half` (0 = low) of each word, low word's element in the low half
-            return half == 0 ? ((lo_word & 0xffffu) | (hi_word << 16)) : ((lo_word >> 16) | (hi_word & 0xffff0000u));
+            __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds_wave, 16, 0, 0);
         }
 
         // max / sum of x over lanes l and l ^ 32, in every lane (one VALU swap,
@@ -102,9 +111,12 @@ namespace q3k
         {
             constexpr int PW = 32 / G; // query positions per wave
             constexpr int QP = 4 * PW; // per block
-            // two buffers: tile t is read from buffer t % 2 while tile t + 1 is
-            // staged from registers into the other after the compute
-            __shared__ __attribute__((aligned(16))) unsigned char lds[2][kTileBytes];
+            // two buffers: a tile is read from one while the next streams from
+            // HBM into the other.  They are separate objects and the loop below
+            // names them statically, so the compiler can tell that the LDS reads
+            // of a tile do not depend on the loads in flight.
+            __shared__ __attribute__((aligned(16))) unsigned char lds_a[kTileBytes];
+            __shared__ __attribute__((aligned(16))) unsigned char lds_b[kTileBytes];
 
             const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             const int lane = threadIdx.x % kWave;
@@ -149,49 +161,36 @@ namespace q3k
 
             const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;
             const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;
-            // staging: K rows k_row + 16 x (x < 4), 16-byte chunk k_chunk of each;
-            // V key pairs v_pair and v_pair + 16 (keys 2p, 2p + 1), dims 8 v_chunk .. + 7
-            const int k_row = threadIdx.x / 16, k_chunk = threadIdx.x % 16;
-            const int v_chunk = threadIdx.x / 16, v_pair = threadIdx.x % 16;
-            Vec8 kst[4], vst[4];
-            auto load_tile = [&](int tile) {
+            // staging: wave w fills rows 16 w .. 16 w + 15 of the K and V halves
+            // of a buffer, kRowsPerLoad rows per load; lane j lands in slot
+            // j % 16 of row j / 16 and so fetches the chunk that slot holds.
+            // Rows past the causal range repeat the last key (finite data, later
+            // masked or weighted by zero).
+            const int st_row = 16 * wave + lane / 16, st_slot = lane % 16;
+            auto issue_tile = [&](int tile, unsigned char *buf) {
                 const int32_t key0 = tile * kKeyTile;
-                const Vec8 zero = {{0u, 0u, 0u, 0u}};
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
+                for (int x = 0; x < 16 / kRowsPerLoad; ++x)
                 {
-                    const int32_t key = key0 + k_row + 16 * x;
-                    kst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(kbase + key * a.ks1) + k_chunk)
-                                          : zero;
-                }
-#pragma unroll
-                for (int x = 0; x < 4; ++x)
-                {
-                    const int32_t key = key0 + 2 * (v_pair + 16 * (x / 2)) + x % 2;
-                    vst[x] = key < n_keys ? load8<false>(reinterpret_cast<const Vec8 *>(vbase + key * a.vs1) + v_chunk)
-                                          : zero;
+                    const int r = st_row + kRowsPerLoad * x;
+                    const int32_t key = key0 + r < n_keys ? key0 + r : n_keys - 1;
+                    unsigned char *dst = buf + (16 * wave + kRowsPerLoad * x) * kRowBytes;
+                    dma16(kbase + key * a.ks1 + 8 * k_slot(r, st_slot), dst);
+                    dma16(vbase + key * a.vs1 + 8 * v_slot(r, st_slot), dst + kHalfBytes);
                 }
             };
-            auto store_tile = [&](unsigned char *buf) {
-                unsigned char *k_lds = buf;
-                unsigned char *vt_lds = buf + kKTileBytes;
+            // per-lane LDS byte offsets of the fragments: K rows li (+ 32 hh),
+            // chunk 2 c + lg, two 8-byte halves; V transpose reads: the lanes of
+            // each 16 give rows 4 lg + j / 4 (+ 8 per 8-key step) and 4 dims
+            // 32 dt + 16 ((lane / 16) % 2) + 4 (j % 4) .. + 3, and each lane gets
+            // 4 consecutive keys of one dim (dim 32 dt + li)
+            const int tj = lane % 16;
+            const int v_row = 4 * lg + tj / 4;
+            int v_off[kAttD / 32];
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    *reinterpret_cast<Vec8 *>(k_lds + (k_row + 16 * x) * kKRowBytes + k_chunk * 16) = kst[x];
-#pragma unroll
-                for (int y = 0; y < 2; ++y)
-                {
-                    const int kk = 2 * (v_pair + 16 * y);
-                    const int pos = (kk & 32) | vt_pos(kk & 31);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                    {
-                        const uint32_t w = bf_pair(vst[2 * y].d[e / 2], vst[2 * y + 1].d[e / 2], e % 2);
-                        *reinterpret_cast<uint32_t *>(vt_lds + (8 * v_chunk + e) * kVtRowBytes + pos * 2) = w;
-                    }
-                }
-            };
-
+            for (int dt = 0; dt < kAttD / 32; ++dt)
+                v_off[dt] = v_row * kRowBytes + 16 * v_slot(v_row, 4 * dt + 2 * ((lane / 16) % 2) + (tj % 4) / 2) +
+                            8 * (tj % 2);
             f32x16_t o[kAttD / 32];
 #pragma unroll
             for (int dt = 0; dt < kAttD / 32; ++dt)
@@ -199,19 +198,11 @@ namespace q3k
             float m = -__builtin_huge_valf(), l = 0.0f;
             const float scale2 = a.scale * kLog2e;
 
-            if (tile_begin < ntiles)
-            {
-                load_tile(tile_begin);
-                store_tile(lds[tile_begin % 2]);
-            }
-            __syncthreads();
-            for (int tile = tile_begin; tile < ntiles; ++tile)
-            {
-                const bool more = tile + 1 < ntiles;
-                if (more)
-                    load_tile(tile + 1); // in flight while this tile is computed
-                const unsigned char *k_lds = lds[tile % 2];
-                const unsigned char *vt_lds = lds[tile % 2] + kKTileBytes;
+            auto step = [&](int tile, const unsigned char *cur, unsigned char *next) {
+                if (tile + 1 < ntiles)
+                    issue_tile(tile + 1, next); // in flight while this tile is computed
+                const unsigned char *k_lds = cur;
+                const unsigned char *v_lds = cur + kHalfBytes;
                 if (wave_active)
                 {
                     const int32_t key0 = tile * kKeyTile;
@@ -221,8 +212,8 @@ namespace q3k
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh)
                         {
-                            const Vec8 kf = *reinterpret_cast<const Vec8 *>(k_lds + (32 * hh + li) * kKRowBytes +
-                                                                             (16 * c + 8 * lg) * 2);
+                            const unsigned char *kp = k_lds + (32 * hh + li) * kRowBytes + 16 * k_slot(li, 2 * c + lg);
+                            const Vec8 kf = *reinterpret_cast<const Vec8 *>(kp);
                             sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kf), qf[c], sacc[hh], 0, 0, 0);
                         }
 
@@ -294,17 +285,31 @@ namespace q3k
 #pragma unroll
                             for (int mm = 0; mm < 2; ++mm)
                             {
-                                const Vec8 vf = *reinterpret_cast<const Vec8 *>(
-                                    vt_lds + (dt * 32 + li) * kVtRowBytes + (32 * hh + 16 * mm + 8 * lg) * 2);
-                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), phi[hh][mm], o[dt], 0, 0,
-                                                                                0);
-                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), plo[hh][mm], o[dt], 0, 0,
-                                                                                0);
+                                // keys 32 hh + 16 mm + 8 t + 4 lg + 0..3 in elements 4 t .. 4 t + 3:
+                                // the keys of the P^T elements this lane holds
+                                const unsigned char *vp = v_lds + v_off[dt] + (32 * hh + 16 * mm) * kRowBytes;
+                                const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp));
+                                const bf16x4_t v1 =
+                                    __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp + 8 * kRowBytes));
+                                const bf16x8_t vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, phi[hh][mm], o[dt], 0, 0, 0);
+                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, plo[hh][mm], o[dt], 0, 0, 0);
                             }
                 }
-                if (more)
-                    store_tile(lds[(tile + 1) % 2]);
-                __syncthreads(); // tile + 1 is staged; every wave is done with tile
+                // this wave's loads of tile + 1 have landed; after the barrier all
+                // have, and every wave is done with tile
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            };
+            if (tile_begin < ntiles)
+                issue_tile(tile_begin, lds_a);
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            for (int tile = tile_begin; tile < ntiles; tile += 2)
+            {
+                step(tile, lds_a, lds_b);
+                if (tile + 1 < ntiles)
+                    step(tile + 1, lds_b, lds_a);
             }
 
             if (!col_ok)
