@@ -21,7 +21,7 @@
 //                 output ulp.
 // Scores are scaled by scale * log2(e) and exponentiated with v_exp_f32.
 // Keys go in tiles of 64 (two S^T halves of 32).  A tile's K and V rows go
-// from HBM straight into LDS (global_load_lds_dwordx4, no registers) while
+// from HBM straight into LDS (buffer_load_dwordx4 ... lds, no registers) while
 // the previous tile is computed, into the other of two buffers; one barrier
 // per tile.  Tile rows are 256 bytes with the 16-byte chunks XOR-swizzled by
 // row so that the K fragment reads (ds_read_b128) and the V transpose reads
@@ -30,6 +30,8 @@
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
 // keys in order, lanes over the head dimension -- the reference's own
 // structure with wave reductions.
+#include <type_traits>
+
 #include "q3k_common.hpp"
 
 namespace q3k
@@ -49,6 +51,7 @@ namespace q3k
         constexpr int kHalfBytes = kKeyTile * kRowBytes;      // the K (or V) rows of a tile
         constexpr int kTileBytes = 2 * kHalfBytes;            // K rows, then V rows
         constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
+        constexpr int kAhead = 2;                             // LDS fragment reads in flight ahead of use
         constexpr float kLog2e = 1.4426950408889634f;
 
         struct AttnArgs
@@ -87,10 +90,28 @@ namespace q3k
         __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
         __device__ __forceinline__ int v_slot(int r, int c) { return c ^ (4 * (r & 3)); }
 
-        // 16 bytes per lane from global memory into LDS at lds_wave + 16 * lane
-        __device__ __forceinline__ void dma16(const void *src, unsigned char *lds_wave)
+        // Buffer resource over [base, base + 2 GiB): raw (stride 0), so the
+        // offsets the loads give are byte offsets from base.
+        __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base)
         {
-            __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds_wave, 16, 0, 0);
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+        }
+
+        // 16 bytes per lane from rsrc + voffset into LDS at lds_wave + 16 * lane
+        // (buffer_load_dwordx4 ... lds: no registers, the wave's LDS base in M0)
+        __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int32_t voffset, unsigned char *lds_wave)
+        {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds_wave, 16, voffset, 0, 0, 0);
+        }
+
+        // Renumbers workgroup ids so that the ids one XCD receives (id % kXcds
+        // == x, in dispatch order) become the contiguous range of the x-th
+        // share of the grid.
+        constexpr unsigned kXcds = 8;
+        __device__ __forceinline__ int xcd_contiguous(unsigned id, unsigned n)
+        {
+            const unsigned x = id % kXcds, k = id / kXcds, q = n / kXcds, r = n % kXcds;
+            return static_cast<int>(x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k);
         }
 
         // max / sum of x over lanes l and l ^ 32, in every lane (one VALU swap,
@@ -111,19 +132,29 @@ namespace q3k
         {
             constexpr int PW = 32 / G; // query positions per wave
             constexpr int QP = 4 * PW; // per block
-            // two buffers: a tile is read from one while the next streams from
-            // HBM into the other.  They are separate objects and the loop below
-            // names them statically, so the compiler can tell that the LDS reads
-            // of a tile do not depend on the loads in flight.
-            __shared__ __attribute__((aligned(16))) unsigned char lds_a[kTileBytes];
-            __shared__ __attribute__((aligned(16))) unsigned char lds_b[kTileBytes];
+            // K and V tiles, two buffers each.  Tile t's P V product is issued in
+            // step t + 1, beside the softmax of tile t + 1, so V(t) stays resident
+            // one step longer than K(t); V(t + 1) is loaded into V(t - 1)'s buffer
+            // once every wave has passed the barrier that ends step t.  The four
+            // buffers are separate objects and the loop below names them
+            // statically, so the compiler can tell that the LDS reads of a step do
+            // not depend on the loads in flight.
+            __shared__ __attribute__((aligned(16))) unsigned char k_a[kHalfBytes];
+            __shared__ __attribute__((aligned(16))) unsigned char k_b[kHalfBytes];
+            __shared__ __attribute__((aligned(16))) unsigned char v_a[kHalfBytes];
+            __shared__ __attribute__((aligned(16))) unsigned char v_b[kHalfBytes];
 
             const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             const int lane = threadIdx.x % kWave;
             const int li = lane % 32, lg = lane / 32;
 
-            // block -> (key slice, batch, KV head, query block); the longest query blocks go first
-            int bid = blockIdx.x;
+            // block -> (key slice, batch, KV head, query block); the longest query
+            // blocks go first.  Workgroups are dealt to the XCDs in turn; when
+            // several query blocks read the same keys, block ids are renumbered to
+            // give each XCD a contiguous run, so the query blocks of one (batch,
+            // KV head) share that XCD's L2.  (Decode blocks share nothing and keep
+            // the plain order, which spreads each batch row over the XCDs.)
+            int bid = a.qblocks > 1 ? xcd_contiguous(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
             const int sp = bid % a.splits;
             bid /= a.splits;
             const int qb = a.qblocks - 1 - bid % a.qblocks;
@@ -164,20 +195,48 @@ namespace q3k
             // staging: wave w fills rows 16 w .. 16 w + 15 of the K and V halves
             // of a buffer, kRowsPerLoad rows per load; lane j lands in slot
             // j % 16 of row j / 16 and so fetches the chunk that slot holds.
-            // Rows past the causal range repeat the last key (finite data, later
-            // masked or weighted by zero).
+            // A tile's loads address from a buffer resource based at its first
+            // key, so the per-lane byte offsets stay fixed (32-bit: checked by
+            // the launcher).  Rows past the causal range repeat the last key
+            // (finite data, later masked or weighted by zero).
             const int st_row = 16 * wave + lane / 16, st_slot = lane % 16;
-            auto issue_tile = [&](int tile, unsigned char *buf) {
-                const int32_t key0 = tile * kKeyTile;
+            const int32_t kstride = static_cast<int32_t>(a.ks1) * 2, vstride = static_cast<int32_t>(a.vs1) * 2;
+            int32_t k_voff[16 / kRowsPerLoad], v_voff[16 / kRowsPerLoad];
 #pragma unroll
-                for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+            for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+            {
+                const int r = st_row + kRowsPerLoad * x;
+                k_voff[x] = r * kstride + 16 * k_slot(r, st_slot);
+                v_voff[x] = r * vstride + 16 * v_slot(r, st_slot);
+            }
+            auto issue_rows = [&](int tile, unsigned char *buf, const uint16_t *base, int64_t row_stride,
+                                  int32_t byte_stride, const int32_t *voff, auto slot) {
+                const int32_t key0 = tile * kKeyTile;
+                const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + static_cast<int64_t>(key0) * row_stride);
+                unsigned char *dst = buf + 16 * wave * kRowBytes;
+                if (key0 + kKeyTile <= n_keys)
                 {
-                    const int r = st_row + kRowsPerLoad * x;
-                    const int32_t key = key0 + r < n_keys ? key0 + r : n_keys - 1;
-                    unsigned char *dst = buf + (16 * wave + kRowsPerLoad * x) * kRowBytes;
-                    dma16(kbase + key * a.ks1 + 8 * k_slot(r, st_slot), dst);
-                    dma16(vbase + key * a.vs1 + 8 * v_slot(r, st_slot), dst + kHalfBytes);
+#pragma unroll
+                    for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+                        dma16(rs, voff[x], dst + kRowsPerLoad * x * kRowBytes);
                 }
+                else
+                {
+                    const int last = n_keys - 1 - key0;
+#pragma unroll
+                    for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+                    {
+                        const int r = st_row + kRowsPerLoad * x;
+                        const int rr = r < last ? r : last;
+                        dma16(rs, rr * byte_stride + 16 * slot(r, st_slot), dst + kRowsPerLoad * x * kRowBytes);
+                    }
+                }
+            };
+            auto issue_k = [&](int tile, unsigned char *buf) {
+                issue_rows(tile, buf, kbase, a.ks1, kstride, k_voff, [](int r, int c) { return k_slot(r, c); });
+            };
+            auto issue_v = [&](int tile, unsigned char *buf) {
+                issue_rows(tile, buf, vbase, a.vs1, vstride, v_voff, [](int r, int c) { return v_slot(r, c); });
             };
             // per-lane LDS byte offsets of the fragments: K rows li (+ 32 hh),
             // chunk 2 c + lg, two 8-byte halves; V transpose reads: the lanes of
@@ -198,24 +257,69 @@ namespace q3k
             float m = -__builtin_huge_valf(), l = 0.0f;
             const float scale2 = a.scale * kLog2e;
 
-            auto step = [&](int tile, const unsigned char *cur, unsigned char *next) {
+            // O^T += V^T P^T for one tile: step i covers the 16-key chunk i / 4
+            // (hh = i / 8, mm = (i / 4) % 2) and dims 32 (i % 4) .. + 31.  The
+            // transpose reads run kAhead steps ahead of the MFMAs that use them.
+            auto read_v = [&](const unsigned char *v_lds, int i) {
+                // keys 16 (i / 4) + 8 t + 4 lg + 0..3 in elements 4 t .. 4 t + 3:
+                // the keys of the P^T elements this lane holds
+                const unsigned char *vp = v_lds + v_off[i % 4] + 16 * (i / 4) * kRowBytes;
+                const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp));
+                const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp + 8 * kRowBytes));
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            bf16x8_t phi[2][2], plo[2][2]; // P of the tile whose P V is still to be issued
+            auto pv = [&](const unsigned char *v_lds) {
+                bf16x8_t vq[kAhead + 1];
+#pragma unroll
+                for (int i = 0; i < kAhead; ++i)
+                    vq[i] = read_v(v_lds, i);
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                {
+                    if (i + kAhead < 16)
+                        vq[(i + kAhead) % (kAhead + 1)] = read_v(v_lds, i + kAhead);
+                    const int dt = i % 4, hh = i / 8, mm = (i / 4) % 2;
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], phi[hh][mm], o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], plo[hh][mm], o[dt], 0, 0, 0);
+                }
+            };
+
+            // One step: load K(tile + 1); S^T = K(tile) Q^T; the P V of the
+            // previous tile (WITH_PV) interleaved with this tile's softmax; after
+            // the barrier, load V(tile + 1) into v_prev.
+            auto step = [&](auto with_pv, int tile, const unsigned char *k_cur, unsigned char *k_next,
+                            unsigned char *v_prev) {
                 if (tile + 1 < ntiles)
-                    issue_tile(tile + 1, next); // in flight while this tile is computed
-                const unsigned char *k_lds = cur;
-                const unsigned char *v_lds = cur + kHalfBytes;
+                    issue_k(tile + 1, k_next); // in flight while this tile is computed
+                const unsigned char *k_lds = k_cur;
                 if (wave_active)
                 {
                     const int32_t key0 = tile * kKeyTile;
+                    auto read_k = [&](int c, int hh) {
+                        return *reinterpret_cast<const Vec8 *>(k_lds + (32 * hh + li) * kRowBytes +
+                                                               16 * k_slot(li, 2 * c + lg));
+                    };
                     f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+                    Vec8 kq[kAhead + 1][2];
 #pragma unroll
-                    for (int c = 0; c < kAttD / 16; ++c)
+                    for (int c = 0; c < kAhead; ++c)
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh)
-                        {
-                            const unsigned char *kp = k_lds + (32 * hh + li) * kRowBytes + 16 * k_slot(li, 2 * c + lg);
-                            const Vec8 kf = *reinterpret_cast<const Vec8 *>(kp);
-                            sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kf), qf[c], sacc[hh], 0, 0, 0);
-                        }
+                            kq[c][hh] = read_k(c, hh);
+#pragma unroll
+                    for (int c = 0; c < kAttD / 16; ++c)
+                    {
+                        if (c + kAhead < kAttD / 16)
+#pragma unroll
+                            for (int hh = 0; hh < 2; ++hh)
+                                kq[(c + kAhead) % (kAhead + 1)][hh] = read_k(c + kAhead, hh);
+                        __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of these MFMAs
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+                            sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kq[c % (kAhead + 1)][hh]), qf[c],
+                                                                               sacc[hh], 0, 0, 0);
+                    }
 
                     // Masked scores become -inf before the max; the max of the raw
                     // scores times the (positive) scale is the max of the scaled ones.
@@ -231,6 +335,8 @@ namespace q3k
                                     sacc[hh][r] = -__builtin_huge_valf();
                             }
                     }
+                    if constexpr (decltype(with_pv)::value)
+                        pv(v_prev); // the previous tile's P V, independent of the softmax below
                     float mloc = sacc[0][0];
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
@@ -241,7 +347,6 @@ namespace q3k
                     const float m_new = fmaxf(m, mloc * scale2);
                     const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
                     const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-                    bf16x8_t phi[2][2], plo[2][2];
                     float psum = 0.0f;
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
@@ -268,8 +373,23 @@ namespace q3k
                     psum = pair_sum(psum);
                     l = l * alpha + psum;
                     m = m_new;
-                    // the running max rarely moves after the first tiles: multiplying
-                    // by alpha == 1 changes nothing, so the wave skips it then
+                    if constexpr (decltype(with_pv)::value)
+                    {
+                        // interleave: two transpose reads, then MFMA and softmax VALU
+                        // work in turn, so the matrix pipe runs under the softmax
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                        {
+                            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); // DS reads
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); // VALU
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                        }
+                    }
+                    // o now holds the tiles before this one at the previous running
+                    // max; the running max rarely moves after the first tiles, and
+                    // multiplying by alpha == 1 changes nothing, so the wave skips it
                     if (__any(alpha != 1.0f))
                     {
 #pragma unroll
@@ -278,38 +398,37 @@ namespace q3k
                             for (int r = 0; r < 16; ++r)
                                 o[dt][r] *= alpha;
                     }
-#pragma unroll
-                    for (int dt = 0; dt < kAttD / 32; ++dt)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                            for (int mm = 0; mm < 2; ++mm)
-                            {
-                                // keys 32 hh + 16 mm + 8 t + 4 lg + 0..3 in elements 4 t .. 4 t + 3:
-                                // the keys of the P^T elements this lane holds
-                                const unsigned char *vp = v_lds + v_off[dt] + (32 * hh + 16 * mm) * kRowBytes;
-                                const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp));
-                                const bf16x4_t v1 =
-                                    __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp + 8 * kRowBytes));
-                                const bf16x8_t vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, phi[hh][mm], o[dt], 0, 0, 0);
-                                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, plo[hh][mm], o[dt], 0, 0, 0);
-                            }
                 }
-                // this wave's loads of tile + 1 have landed; after the barrier all
-                // have, and every wave is done with tile
+                // this wave's loads of K(tile + 1) and V(tile) have landed; after the
+                // barrier all have, and every wave is done with K(tile) and V(tile - 1)
                 __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
-            };
-            if (tile_begin < ntiles)
-                issue_tile(tile_begin, lds_a);
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            for (int tile = tile_begin; tile < ntiles; tile += 2)
-            {
-                step(tile, lds_a, lds_b);
                 if (tile + 1 < ntiles)
-                    step(tile + 1, lds_b, lds_a);
+                    issue_v(tile + 1, v_prev);
+            };
+            using no_pv = std::integral_constant<bool, false>;
+            using with_pv = std::integral_constant<bool, true>;
+            if (tile_begin < ntiles)
+            {
+                issue_k(tile_begin, k_a);
+                issue_v(tile_begin, v_a);
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                // V(t) sits in v_a when t - tile_begin is even, else in v_b
+                step(no_pv{}, tile_begin, k_a, k_b, v_b);
+                for (int tile = tile_begin + 1; tile < ntiles; tile += 2)
+                {
+                    step(with_pv{}, tile, k_b, k_a, v_a);
+                    if (tile + 1 < ntiles)
+                        step(with_pv{}, tile + 1, k_a, k_b, v_b);
+                }
+                if (wave_active)
+                {
+                    if ((ntiles - 1 - tile_begin) % 2 == 0)
+                        pv(v_a);
+                    else
+                        pv(v_b);
+                }
             }
 
             if (!col_ok)
@@ -441,7 +560,10 @@ namespace q3k
         bool mfma_ok(const AttnArgs &a, int32_t G)
         {
             const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32;
-            return g_ok && a.D == kAttD && a.start + a.S <= INT32_MAX && a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
+            // tile loads use 32-bit byte offsets of up to kKeyTile rows
+            const int64_t row_limit = (INT32_MAX - kRowBytes) / (2 * kKeyTile);
+            return g_ok && a.D == kAttD && a.start + a.S <= INT32_MAX && a.ks1 <= row_limit && a.vs1 <= row_limit &&
+                   a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
                    a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 && aligned16(a.q) &&
                    aligned16(a.k) && aligned16(a.v) && aligned_to(a.out, 8);
         }
