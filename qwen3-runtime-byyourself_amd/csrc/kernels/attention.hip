@@ -23,9 +23,12 @@
 // Keys go in tiles of 64 (two S^T halves of 32).  A tile's K and V rows go
 // from HBM straight into LDS (buffer_load_dwordx4 ... lds, no registers) while
 // the previous tile is computed, into the other of two buffers; one barrier
-// per tile.  Tile rows are 256 bytes with the 16-byte chunks XOR-swizzled by
+// per tile.  The P V product of a tile is issued in the next tile's step,
+// interleaved with that tile's softmax, so the matrix pipe runs under the
+// VALU work.  Tile rows are 256 bytes with the 16-byte chunks XOR-swizzled by
 // row so that the K fragment reads (ds_read_b128) and the V transpose reads
-// hit distinct LDS banks.
+// hit distinct LDS banks.  Prefill grids are renumbered so that the query
+// blocks of one (batch, KV head) run on one XCD and share its L2.
 //
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
 // keys in order, lanes over the head dimension -- the reference's own
@@ -52,6 +55,9 @@ namespace q3k
         constexpr int kTileBytes = 2 * kHalfBytes;            // K rows, then V rows
         constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
         constexpr int kAhead = 2;                             // LDS fragment reads in flight ahead of use
+        constexpr int kAttWaves = 4;                          // waves per matrix-core block
+        constexpr int kAttBlock = kAttWaves * kWave;
+        constexpr int kStageRows = kKeyTile / kAttWaves;      // K (and V) rows of a tile each wave loads
         constexpr float kLog2e = 1.4426950408889634f;
 
         struct AttnArgs
@@ -128,10 +134,10 @@ namespace q3k
         }
 
         template <int G>
-        __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(AttnArgs a)
+        __global__ __launch_bounds__(kAttBlock) void attn_mfma_kernel(AttnArgs a)
         {
             constexpr int PW = 32 / G; // query positions per wave
-            constexpr int QP = 4 * PW; // per block
+            constexpr int QP = kAttWaves * PW; // per block
             // K and V tiles, two buffers each.  Tile t's P V product is issued in
             // step t + 1, beside the softmax of tile t + 1, so V(t) stays resident
             // one step longer than K(t); V(t + 1) is loaded into V(t - 1)'s buffer
@@ -192,18 +198,18 @@ namespace q3k
 
             const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;
             const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;
-            // staging: wave w fills rows 16 w .. 16 w + 15 of the K and V halves
-            // of a buffer, kRowsPerLoad rows per load; lane j lands in slot
+            // staging: wave w fills rows kStageRows w .. + kStageRows - 1 of a K
+            // (or V) buffer, kRowsPerLoad rows per load; lane j lands in slot
             // j % 16 of row j / 16 and so fetches the chunk that slot holds.
             // A tile's loads address from a buffer resource based at its first
             // key, so the per-lane byte offsets stay fixed (32-bit: checked by
             // the launcher).  Rows past the causal range repeat the last key
             // (finite data, later masked or weighted by zero).
-            const int st_row = 16 * wave + lane / 16, st_slot = lane % 16;
+            const int st_row = kStageRows * wave + lane / 16, st_slot = lane % 16;
             const int32_t kstride = static_cast<int32_t>(a.ks1) * 2, vstride = static_cast<int32_t>(a.vs1) * 2;
-            int32_t k_voff[16 / kRowsPerLoad], v_voff[16 / kRowsPerLoad];
+            int32_t k_voff[kStageRows / kRowsPerLoad], v_voff[kStageRows / kRowsPerLoad];
 #pragma unroll
-            for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+            for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
             {
                 const int r = st_row + kRowsPerLoad * x;
                 k_voff[x] = r * kstride + 16 * k_slot(r, st_slot);
@@ -213,18 +219,18 @@ namespace q3k
                                   int32_t byte_stride, const int32_t *voff, auto slot) {
                 const int32_t key0 = tile * kKeyTile;
                 const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + static_cast<int64_t>(key0) * row_stride);
-                unsigned char *dst = buf + 16 * wave * kRowBytes;
+                unsigned char *dst = buf + kStageRows * wave * kRowBytes;
                 if (key0 + kKeyTile <= n_keys)
                 {
 #pragma unroll
-                    for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+                    for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
                         dma16(rs, voff[x], dst + kRowsPerLoad * x * kRowBytes);
                 }
                 else
                 {
                     const int last = n_keys - 1 - key0;
 #pragma unroll
-                    for (int x = 0; x < 16 / kRowsPerLoad; ++x)
+                    for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
                     {
                         const int r = st_row + kRowsPerLoad * x;
                         const int rr = r < last ? r : last;
@@ -584,7 +590,7 @@ namespace q3k
         {
             SplitPlan p;
             const int32_t G = Hq / Hkv;
-            const int64_t QP = 4 * (32 / (G > 32 ? 32 : G));
+            const int64_t QP = kAttWaves * (32 / (G > 32 ? 32 : G));
             const int64_t blocks = B * Hkv * ((S + QP - 1) / QP);
             if (blocks >= kSplitTargetBlocks || cached < 2 * kMinSplitKeys)
                 return p;
@@ -609,10 +615,10 @@ namespace q3k
         template <int G>
         void launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
         {
-            constexpr int QP = 4 * (32 / G);
+            constexpr int QP = kAttWaves * (32 / G);
             a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
-            attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream>>>(a);
+            attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kAttBlock), 0, stream>>>(a);
             if (a.splits > 1)
                 attn_combine_kernel<<<dim3(static_cast<unsigned>((a.rows + 3) / 4)), dim3(kBlock), 0, stream>>>(
                     a.part_o, a.part_ml, a.out, a.rows, a.splits);
