@@ -399,6 +399,8 @@ def test_kv_append_kat(q3k, hip, oracle):
     (2, 7, 1024, 2, 11, 1, np.uint16, 2),      # unaligned pointers: 2-byte words
     (2, 4, 1024, 2, 4, 0, np.float32, 4),      # fp32, 4-byte aligned: 4-byte words
     (1, 300, 256, 1, 300, 0, np.uint16, 0),    # full capacity in one append
+    (3, 5, 1024, 3, 8, 2, np.uint16, 0),       # 15 tokens: not a whole number of 4-token blocks
+    (5, 3, 128, 6, 7, 4, np.uint16, 0),        # S below the tokens per block: one block spans batch rows
 ])
 def test_kv_append_shapes(q3k, hip, oracle, synth, B, S, row, Bc, Sc, start, dtype, offset):
     name = f"kv_append B={B} S={S} row={row} cap=({Bc},{Sc}) start={start} {np.dtype(dtype).name} offset={offset}"
