@@ -595,7 +595,9 @@ def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset):
 # ---------------------------------------------------------------- sampling: top-k candidates
 
 @pytest.mark.parametrize("rows,N,valid,k", [(8, 151936, 0, 20), (4, 151936, 151669, 1), (2, 151936, 0, 1024),
-                                           (3, 5000, 0, 64), (2, 513, 500, 3)])
+                                           (3, 5000, 0, 64), (2, 513, 500, 3),
+                                           (2, 600, 0, 100),      # fewer than k threads hold logits: all listed
+                                           (2, 20000, 0, 1500)])  # k above the thread count: whole-row select
 def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k):
     """GPU top-k selection (the reference sampler's top-k rule, sampler.cpp:160-190): the candidate set equals the
     oracle's exactly, ties at the k-th included; non-finite rows flagged."""
