@@ -55,6 +55,7 @@ namespace q3k
         constexpr int kTileBytes = 2 * kHalfBytes;            // K rows, then V rows
         constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
         constexpr int kAhead = 2;                             // LDS fragment reads in flight ahead of use
+        constexpr float kLazyMax = 8.0f;                      // log2 headroom before the softmax reference moves
         constexpr int kAttWaves = 4;                          // waves per matrix-core block
         constexpr int kAttBlock = kAttWaves * kWave;
         constexpr int kStageRows = kKeyTile / kAttWaves;      // K (and V) rows of a tile each wave loads
@@ -77,7 +78,7 @@ namespace q3k
             float scale;
             // split-K: the key range is cut into `splits` slices of split_keys
             // keys (a multiple of the tile); slice results (unnormalised O^T,
-            // running max and sum) go to part_o [splits, rows, D] and part_ml
+            // reference max and sum) go to part_o [splits, rows, D] and part_ml
             // [splits, rows, 2] and attn_combine_kernel merges them
             int32_t splits;
             int32_t split_keys;
@@ -350,9 +351,16 @@ namespace q3k
                         for (int r = 0; r < 16; ++r)
                             mloc = fmaxf(mloc, sacc[hh][r]);
                     mloc = pair_max(mloc);
-                    const float m_new = fmaxf(m, mloc * scale2);
+                    // The weights are taken relative to a reference m that moves
+                    // only when a tile's max exceeds it by more than kLazyMax
+                    // (log2 units): the weights stay below 2^kLazyMax, and the
+                    // rescale of o (alpha != 1) is left for the rare tiles that
+                    // move it.  An all-masked column keeps m = -inf and weight 0.
+                    const float m_tile = mloc * scale2;
+                    const bool move = m_tile > m + kLazyMax;
+                    const float m_new = move ? m_tile : m;
                     const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
-                    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+                    const float alpha = move ? __builtin_amdgcn_exp2f(m - m_use) : 1.0f;
                     float psum = 0.0f;
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
@@ -393,9 +401,9 @@ namespace q3k
                             __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
                         }
                     }
-                    // o now holds the tiles before this one at the previous running
-                    // max; the running max rarely moves after the first tiles, and
-                    // multiplying by alpha == 1 changes nothing, so the wave skips it
+                    // o now holds the tiles before this one at the previous reference;
+                    // it rarely moves after the first tile, and multiplying by
+                    // alpha == 1 changes nothing, so the wave skips it then
                     if (__any(alpha != 1.0f))
                     {
 #pragma unroll
@@ -474,7 +482,7 @@ namespace q3k
         }
 
         // Merges the key slices of one query row per wave: weights
-        // 2^(m_s - max m) (the running maxima are in the log2 domain), then
+        // 2^(m_s - max m) (the reference maxima are in the log2 domain), then
         // sum_s w_s O_s / sum_s w_s l_s; lane t holds dims 2t, 2t + 1.
         __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__restrict__ part_o,
                                                                       const float *__restrict__ part_ml,
