@@ -542,6 +542,31 @@ def test_gqa_attention(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, D, cap, of
     check_band(oracle, name, got, prim, lo, hi)
 
 
+@pytest.mark.parametrize("B,S,start,cap,split", [(2, 200, 100, 320, False), (1, 1, 700, 704, True),
+                                                   (1, 70, 400, 480, False)])
+def test_gqa_attention_score_spikes(q3k, hip, oracle, synth, B, S, start, cap, split):
+    """Keys parallel to a query row raise the scores of later tiles far above the earlier ones (by 2^10 and more in
+    the exponent), so the softmax reference of the kernel moves mid-sequence and the output accumulators are
+    rescaled; with split, inside key slices that the merge then weighs."""
+    Hq, Hkv, D = 32, 8, 128
+    name = f"gqa_attention spikes B={B} S={S} start={start} split={split}"
+    announce(name)
+    q = synth.normal_bf16(170, S, (B, S, Hq * D))
+    store_k = synth.normal_bf16(171, S, (B, cap, Hkv, D))
+    store_v = synth.normal_bf16(172, S, (B, cap, Hkv, D))
+    qf = (q.astype(np.uint32) << 16).view(np.float32).reshape(B, S, Hq, D)
+    L = start + S
+    for b in range(B):
+        for n, (key, scale) in enumerate(((L // 3, 1.0), (L // 2, 1.5), (L - 2, 2.0))):
+            s_ref = min(S - 1, n * S // 3)
+            for kvh in range(Hkv):
+                h = kvh * (Hq // Hkv) + n % (Hq // Hkv)
+                store_k[b, key, kvh] = synth.f32_to_bf16(scale * qf[b, s_ref, h])
+    got = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start, split=split)
+    prim, lo, hi = oracle.gqa_attention(q, store_k[:, :L], store_v[:, :L], Hq, start)
+    check_band(oracle, name, got, prim, lo, hi)
+
+
 @pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
 def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
     """Benchmark-size prefill (config 4 shape, and a 4096-token sequence): every row computed on the GPU, a seeded
