@@ -17,6 +17,16 @@ extern "C" {
  * multiple of 16, both pointers 16-byte aligned, no overlap. */
 Q3K_API int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3k_stream_t stream);
 
+/* Read ceiling of a strided row layout such as a KV-cache view: outer x inner
+ * views, view (o, i) at base + o * outer_stride + i * inner_stride, each
+ * `rows` rows of row_bytes at row_stride (bytes; strides multiples of 16,
+ * row_bytes a power of two from 16 to 4096).  base2 (nullable) is read with
+ * the same layout (keys and values).  One 256-thread block per view; the XOR
+ * of the data goes to sink[view * 256 + thread] (outer * inner * 256 words). */
+Q3K_API int q3k_bench_read_rows_u128(const void *base, const void *base2, int64_t outer, int64_t outer_stride,
+                                     int64_t inner, int64_t inner_stride, int64_t rows, int64_t row_stride,
+                                     int64_t row_bytes, uint32_t *sink, q3k_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,6 +89,7 @@ SIGNATURES = {
                                         _p, _p, _i64, _i64, _p],
     "q3k_build_rope_cache_f32": [_p, _i64, _i32, _f32],
     "q3k_bench_copy_u128": [_p, _p, _i64, _p],
+    "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 
 _lib = None
@@ -234,3 +235,10 @@ def build_rope_cache(P: int, D: int, theta: float):
 
 def bench_copy(src, dst, nbytes, stream=None):
     _check(load().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
+
+
+def bench_read_rows(base, base2, outer, outer_stride, inner, inner_stride, rows, row_stride, row_bytes, sink,
+                    stream=None):
+    """Read ceiling of a strided row layout (q3k_bench.h); all sizes in bytes."""
+    _check(load().q3k_bench_read_rows_u128(_ptr(base), _ptr(base2), outer, outer_stride, inner, inner_stride, rows,
+                                           row_stride, row_bytes, _ptr(sink), _ptr(stream)))

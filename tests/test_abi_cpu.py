@@ -62,8 +62,13 @@ def test_argument_errors_without_gpu(q3k):
     _expect(q3k.qk_norm_rope, IndexError, OR, fake, fake, fake, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 14)
     _expect(q3k.qk_norm_rope, ValueError, IA, fake, fake, fake, fake, 1, 3, 2, 1, 8, -1.0, fake, 16, 0)
     _expect(q3k.qk_norm_rope, ValueError, IA, fake, fake, None, fake, 1, 3, 2, 1, 8, 1e-6, fake, 16, 0)
-    # copy helper
+    # measurement aids
     _expect(q3k.bench_copy, ValueError, IA, fake, fake, 15)
+    _expect(q3k.bench_read_rows, ValueError, IA, fake, None, 2, 4096, 2, 256, 8, 512, 24, fake)    # row not 2^k
+    _expect(q3k.bench_read_rows, ValueError, IA, fake, None, 2, 4096, 2, 8, 8, 512, 256, fake)     # stride % 16
+    _expect(q3k.bench_read_rows, ValueError, IA, None, None, 2, 4096, 2, 256, 8, 512, 256, fake)
+    _expect(q3k.bench_read_rows, ValueError, IA, fake, None, -1, 4096, 2, 256, 8, 512, 256, fake)
+    q3k.bench_read_rows(None, None, 0, 4096, 2, 256, 8, 512, 256, None)
 
 
 def test_empty_inputs_are_no_ops(q3k):

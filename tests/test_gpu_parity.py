@@ -567,6 +567,34 @@ def test_gqa_attention_score_spikes(q3k, hip, oracle, synth, B, S, start, cap, s
     check_band(oracle, name, got, prim, lo, hi)
 
 
+def test_bench_read_rows(q3k, hip):
+    """The read-ceiling aid reads exactly the rows of the views it is given: its per-thread XOR fold matches the
+    same fold computed on the host (KV-cache view layout [B, L, Hkv, D] of keys and values)."""
+    announce("bench_read_rows")
+    B, L, Hkv, D = 3, 300, 4, 128
+    rng = np.random.default_rng(7)
+    k = rng.integers(0, 1 << 32, (B, L, Hkv, D // 2), dtype=np.uint32)
+    v = rng.integers(0, 1 << 32, (B, L, Hkv, D // 2), dtype=np.uint32)
+    K, V = Guarded(hip, k), Guarded(hip, v)
+    sink = Guarded(hip, nbytes=B * Hkv * 256 * 4)
+    q3k.bench_read_rows(K, V, B, L * Hkv * D * 2, Hkv, D * 2, L, Hkv * D * 2, D * 2, sink)
+    hip.synchronize()
+    assert K.guards_intact() and V.guards_intact() and sink.guards_intact()
+    got = sink.get(np.uint32, (B * Hkv, 256))
+    chunks = D * 2 // 16
+    kw, vw = k.reshape(B, L, Hkv, chunks, 4), v.reshape(B, L, Hkv, chunks, 4)
+    want = np.zeros((B * Hkv, 256), np.uint32)
+    for view in range(B * Hkv):
+        b, h = divmod(view, Hkv)
+        for t in range(256):
+            r_in, c = divmod(t, chunks)
+            rows = np.arange(r_in, L, 256 // chunks)
+            x, y = kw[b, rows, h, c], vw[b, rows, h, c]
+            f = ((x[:, 0] + x[:, 3]) ^ (y[:, 1] + y[:, 2])).astype(np.uint32)
+            want[view, t] = np.bitwise_xor.reduce(f) if f.size else 0
+    check_exact("bench_read_rows sink", got, want)
+
+
 @pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
 def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
     """Benchmark-size prefill (config 4 shape, and a 4096-token sequence): every row computed on the GPU, a seeded
