@@ -389,16 +389,20 @@ namespace q3k
                     m = m_new;
                     if constexpr (decltype(with_pv)::value)
                     {
-                        // interleave: two transpose reads, then MFMA and softmax VALU
-                        // work in turn, so the matrix pipe runs under the softmax
+                        // interleave MFMA and softmax VALU work in turn, so the matrix
+                        // pipe runs under the softmax.  The transpose reads keep their
+                        // distance: the first kAhead steps' reads lead, and each step's
+                        // two reads (for step i + kAhead) follow its MFMAs.
+                        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0); // DS reads
 #pragma unroll
                         for (int i = 0; i < 16; ++i)
                         {
-                            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); // DS reads
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
                             __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); // VALU
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                             __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                            if (i + kAhead < 16)
+                                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                         }
                     }
                     // o now holds the tiles before this one at the previous reference;
