@@ -24,10 +24,11 @@
 // from HBM straight into LDS (buffer_load_dwordx4 ... lds, no registers) while
 // the previous tile is computed, into the other of two buffers; one barrier
 // per tile.  The P V product of a tile is issued in the next tile's step,
-// interleaved with that tile's softmax, so the matrix pipe runs under the
-// VALU work.  Tile rows are 256 bytes with the 16-byte chunks XOR-swizzled by
-// row so that the K fragment reads (ds_read_b128) and the V transpose reads
-// hit distinct LDS banks.  Prefill grids are renumbered so that the query
+// beside that tile's softmax; within one wave the matrix cores and the VALU do
+// not overlap on gfx950 (measured), so the overlap comes from the other
+// block's wave on the same SIMD.  Tile rows are 256 bytes with the 16-byte
+// chunks XOR-swizzled by row so that the K fragment reads (ds_read_b128) and
+// the V transpose reads hit distinct LDS banks.  Prefill grids are renumbered so that the query
 // blocks of one (batch, KV head) run on one XCD and share its L2.
 //
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
@@ -58,7 +59,6 @@ namespace q3k
         constexpr float kLazyMax = 8.0f;                      // log2 headroom before the softmax reference moves
         constexpr int kAttWaves = 4;                          // waves per matrix-core block
         constexpr int kAttBlock = kAttWaves * kWave;
-        constexpr int kStageRows = kKeyTile / kAttWaves;      // K (and V) rows of a tile each wave loads
         constexpr float kLog2e = 1.4426950408889634f;
 
         struct AttnArgs
@@ -134,10 +134,302 @@ namespace q3k
             return __uint_as_float(r[0]) + __uint_as_float(r[1]);
         }
 
+        // ---- tile operations shared by the kernels ------------------------------
+
+        // Loading a key tile's K (or V) rows into LDS from a block of WAVES
+        // waves: wave w fills rows (kKeyTile / WAVES) w .. of a buffer,
+        // kRowsPerLoad rows per load; lane j lands in slot j % 16 of row j / 16
+        // and so fetches the chunk that slot holds.  A tile's loads address from
+        // a buffer resource based at its first key, so the per-lane byte offsets
+        // (tile_offsets) stay fixed: 32-bit, checked by the launcher.  Rows past
+        // n_keys repeat the last key (finite data, later masked or weighted by
+        // zero).
+        template <int WAVES>
+        struct Staging
+        {
+            static constexpr int kRows = kKeyTile / WAVES;      // rows of a tile per wave
+            static constexpr int kLoads = kRows / kRowsPerLoad; // loads per wave per K (or V) tile
+        };
+
+        template <int WAVES, typename Slot>
+        __device__ __forceinline__ void tile_offsets(int wave, int lane, int32_t byte_stride, Slot slot,
+                                                     int32_t (&voff)[Staging<WAVES>::kLoads])
+        {
+            const int st_row = Staging<WAVES>::kRows * wave + lane / 16;
+#pragma unroll
+            for (int x = 0; x < Staging<WAVES>::kLoads; ++x)
+            {
+                const int r = st_row + kRowsPerLoad * x;
+                voff[x] = r * byte_stride + 16 * slot(r, lane % 16);
+            }
+        }
+
+        template <int WAVES, typename Slot>
+        __device__ __forceinline__ void load_tile_rows(int tile, unsigned char *buf, const uint16_t *base,
+                                                       int64_t row_stride, int32_t byte_stride, int32_t n_keys,
+                                                       int wave, int lane, const int32_t (&voff)[Staging<WAVES>::kLoads],
+                                                       Slot slot)
+        {
+            constexpr int kRows = Staging<WAVES>::kRows;
+            const int32_t key0 = tile * kKeyTile;
+            const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + static_cast<int64_t>(key0) * row_stride);
+            unsigned char *dst = buf + kRows * wave * kRowBytes;
+            if (key0 + kKeyTile <= n_keys)
+            {
+#pragma unroll
+                for (int x = 0; x < Staging<WAVES>::kLoads; ++x)
+                    dma16(rs, voff[x], dst + kRowsPerLoad * x * kRowBytes);
+            }
+            else
+            {
+                const int last = n_keys - 1 - key0;
+                const int st_row = kRows * wave + lane / 16;
+#pragma unroll
+                for (int x = 0; x < Staging<WAVES>::kLoads; ++x)
+                {
+                    const int r = st_row + kRowsPerLoad * x;
+                    const int rr = r < last ? r : last;
+                    dma16(rs, rr * byte_stride + 16 * slot(r, lane % 16), dst + kRowsPerLoad * x * kRowBytes);
+                }
+            }
+        }
+
+        // both halves of the staging for one kernel: K and V bases, strides and
+        // the per-lane offsets, as lambdas over the kernel's locals
+#define Q3K_ATTN_STAGING(WAVES)                                                                                      \
+    const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;                                                            \
+    const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;                                                            \
+    const int32_t kstride = static_cast<int32_t>(a.ks1) * 2, vstride = static_cast<int32_t>(a.vs1) * 2;               \
+    const auto kslot = [](int r, int c) __attribute__((always_inline)) { return k_slot(r, c); };                                                     \
+    const auto vslot = [](int r, int c) __attribute__((always_inline)) { return v_slot(r, c); };                                                     \
+    int32_t k_voff[Staging<WAVES>::kLoads], v_voff[Staging<WAVES>::kLoads];                                           \
+    tile_offsets<WAVES>(wave, lane, kstride, kslot, k_voff);                                                          \
+    tile_offsets<WAVES>(wave, lane, vstride, vslot, v_voff);                                                          \
+    auto load_k = [&](int tile, unsigned char *buf) __attribute__((always_inline)) {                                                                 \
+        load_tile_rows<WAVES>(tile, buf, kbase, a.ks1, kstride, n_keys, wave, lane, k_voff, kslot);                   \
+    };                                                                                                                \
+    auto load_v = [&](int tile, unsigned char *buf) __attribute__((always_inline)) {                                                                 \
+        load_tile_rows<WAVES>(tile, buf, vbase, a.vs1, vstride, n_keys, wave, lane, v_voff, vslot);                   \
+    };
+
+        // Q fragments of the lane's column.  A padding column (s_col >= S) reads
+        // the last position's row instead: its scores are always masked (a wave
+        // holding one is a partial wave), so only finiteness matters.
+        __device__ __forceinline__ void load_q(const AttnArgs &a, int64_t b, int32_t s_col, int h_col, bool col_ok,
+                                               int lg, bf16x8_t (&qf)[kAttD / 16])
+        {
+            const int64_t s_row = col_ok ? s_col : a.S - 1;
+            const Vec8 *qrow = reinterpret_cast<const Vec8 *>(a.q + ((b * a.S + s_row) * a.Hq + h_col) * kAttD);
+#pragma unroll
+            for (int c = 0; c < kAttD / 16; ++c)
+                qf[c] = as_bf8(qrow[2 * c + lg]);
+        }
+
+        // Per-lane LDS byte offsets of the V transpose reads: the lanes of each
+        // 16 give rows 4 lg + j / 4 (+ 8 per 8-key step) and 4 dims
+        // 32 dt + 16 ((lane / 16) % 2) + 4 (j % 4) .. + 3, and each lane gets 4
+        // consecutive keys of one dim (dim 32 dt + lane % 32).
+        __device__ __forceinline__ void v_offsets(int lane, int (&v_off)[kAttD / 32])
+        {
+            const int tj = lane % 16, lg = lane / 32;
+            const int v_row = 4 * lg + tj / 4;
+#pragma unroll
+            for (int dt = 0; dt < kAttD / 32; ++dt)
+                v_off[dt] = v_row * kRowBytes + 16 * v_slot(v_row, 4 * dt + 2 * ((lane / 16) % 2) + (tj % 4) / 2) +
+                            8 * (tj % 2);
+        }
+
+        // S^T = K Q^T for the 64 keys of a tile (sacc[hh]: keys 32 hh .. + 31).
+        // The K fragment reads run kAhead steps ahead of the MFMAs that use them.
+        __device__ __forceinline__ void qk_tile(const unsigned char *k_lds, const bf16x8_t (&qf)[kAttD / 16], int li,
+                                                int lg, f32x16_t (&sacc)[2])
+        {
+            auto read_k = [&](int c, int hh) __attribute__((always_inline)) {
+                return *reinterpret_cast<const Vec8 *>(k_lds + (32 * hh + li) * kRowBytes +
+                                                       16 * k_slot(li, 2 * c + lg));
+            };
+            sacc[0] = f32x16_t{};
+            sacc[1] = f32x16_t{};
+            Vec8 kq[kAhead + 1][2];
+#pragma unroll
+            for (int c = 0; c < kAhead; ++c)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+                    kq[c][hh] = read_k(c, hh);
+#pragma unroll
+            for (int c = 0; c < kAttD / 16; ++c)
+            {
+                if (c + kAhead < kAttD / 16)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        kq[(c + kAhead) % (kAhead + 1)][hh] = read_k(c + kAhead, hh);
+                __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of these MFMAs
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+                    sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kq[c % (kAhead + 1)][hh]), qf[c], sacc[hh],
+                                                                       0, 0, 0);
+            }
+        }
+
+        // Scores of keys past the column's causal limit and of padding columns
+        // become -inf (before the max).
+        __device__ __forceinline__ void mask_tile(f32x16_t (&sacc)[2], int32_t key0, int lg, int32_t last_key,
+                                                  bool col_ok)
+        {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    const int32_t kk = key0 + 32 * hh + 8 * (r / 4) + 4 * lg + (r % 4);
+                    if (kk > last_key || !col_ok)
+                        sacc[hh][r] = -__builtin_huge_valf();
+                }
+        }
+
+        // Online softmax of one tile for the lane's column: the weights, split
+        // into bf16 high parts and remainders, go to phi / plo, and m, l are
+        // updated.  The weights are taken relative to a reference m that moves
+        // only when a tile's max exceeds it by more than kLazyMax (log2 units):
+        // they stay below 2^kLazyMax, and the rescale of the output is left for
+        // the rare tiles that move it.  Returns that rescale factor (1 when m did
+        // not move).  An all-masked column keeps m = -inf and weight 0.  The max
+        // of the raw scores times the (positive) scale is the max of the scaled
+        // ones.
+        __device__ __forceinline__ float softmax_tile(const f32x16_t (&sacc)[2], float scale2, float &m, float &l,
+                                                      bf16x8_t (&phi)[2][2], bf16x8_t (&plo)[2][2])
+        {
+            float mloc = sacc[0][0];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    mloc = fmaxf(mloc, sacc[hh][r]);
+            mloc = pair_max(mloc);
+            const float m_tile = mloc * scale2;
+            const bool move = m_tile > m + kLazyMax;
+            const float m_new = move ? m_tile : m;
+            const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
+            const float alpha = move ? __builtin_amdgcn_exp2f(m - m_use) : 1.0f;
+            float psum = 0.0f;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm)
+                {
+                    Vec8 h8, l8;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                    {
+                        const float x0 =
+                            __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[hh][8 * mm + 2 * j], scale2, -m_use));
+                        const float x1 =
+                            __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[hh][8 * mm + 2 * j + 1], scale2, -m_use));
+                        psum += x0;
+                        psum += x1;
+                        const uint32_t hp = pack_rne(x0, x1);
+                        h8.d[j] = hp;
+                        l8.d[j] = pack_rne(x0 - bf_lo(hp), x1 - bf_hi(hp));
+                    }
+                    phi[hh][mm] = as_bf8(h8);
+                    plo[hh][mm] = as_bf8(l8);
+                }
+            psum = pair_sum(psum);
+            l = l * alpha + psum;
+            m = m_new;
+            return alpha;
+        }
+
+        // o *= alpha; multiplying by alpha == 1 changes nothing, so the wave
+        // skips it when no lane needs it
+        __device__ __forceinline__ void rescale(f32x16_t (&o)[kAttD / 32], float alpha)
+        {
+            if (__any(alpha != 1.0f))
+            {
+#pragma unroll
+                for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        o[dt][r] *= alpha;
+            }
+        }
+
+        // O^T += V^T P^T for one tile: step i covers the 16-key chunk i / 4
+        // (hh = i / 8, mm = (i / 4) % 2) and dims 32 (i % 4) .. + 31.  The
+        // transpose reads run kAhead steps ahead of the MFMAs that use them.
+        __device__ __forceinline__ void pv_tile(const unsigned char *v_lds, const int (&v_off)[kAttD / 32],
+                                                const bf16x8_t (&phi)[2][2], const bf16x8_t (&plo)[2][2],
+                                                f32x16_t (&o)[kAttD / 32])
+        {
+            auto read_v = [&](int i) __attribute__((always_inline)) {
+                // keys 16 (i / 4) + 8 t + 4 lg + 0..3 in elements 4 t .. 4 t + 3:
+                // the keys of the P^T elements this lane holds
+                const unsigned char *vp = v_lds + v_off[i % 4] + 16 * (i / 4) * kRowBytes;
+                const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp));
+                const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp + 8 * kRowBytes));
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            bf16x8_t vq[kAhead + 1];
+#pragma unroll
+            for (int i = 0; i < kAhead; ++i)
+                vq[i] = read_v(i);
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+            {
+                if (i + kAhead < 16)
+                    vq[(i + kAhead) % (kAhead + 1)] = read_v(i + kAhead);
+                __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of these MFMAs
+                const int dt = i % 4, hh = i / 8, mm = (i / 4) % 2;
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], phi[hh][mm], o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], plo[hh][mm], o[dt], 0, 0, 0);
+            }
+        }
+
+        // The lane's column of the result: bf16 O / l, or with split keys the
+        // slice's unnormalised O^T, reference max and sum for the merge.
+        __device__ __forceinline__ void store_column(const AttnArgs &a, int sp, int64_t b, int32_t s_col, int h_col,
+                                                     int lg, const f32x16_t (&o)[kAttD / 32], float m, float l)
+        {
+            if (a.splits > 1)
+            {
+                const int64_t slot = static_cast<int64_t>(sp) * a.rows + (b * a.S + s_col) * a.Hq + h_col;
+                float *po = a.part_o + slot * kAttD;
+#pragma unroll
+                for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4)
+                    {
+                        const float4 w = {o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+                        *reinterpret_cast<float4 *>(po + dt * 32 + 8 * q4 + 4 * lg) = w;
+                    }
+                if (lg == 0)
+                {
+                    a.part_ml[2 * slot] = m;
+                    a.part_ml[2 * slot + 1] = l;
+                }
+                return;
+            }
+            const float inv = 1.0f / l;
+            uint16_t *orow = a.out + ((b * a.S + s_col) * a.Hq + h_col) * kAttD;
+#pragma unroll
+            for (int dt = 0; dt < kAttD / 32; ++dt)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                {
+                    const int d = dt * 32 + 8 * q4 + 4 * lg;
+                    uint2 w;
+                    w.x = pack_rne(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv);
+                    w.y = pack_rne(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+                    *reinterpret_cast<uint2 *>(orow + d) = w;
+                }
+        }
+
+        // ---- the matrix-core kernel ---------------------------------------------
+
         template <int G>
         __global__ __launch_bounds__(kAttBlock) void attn_mfma_kernel(AttnArgs a)
         {
-            constexpr int PW = 32 / G; // query positions per wave
+            constexpr int PW = 32 / G;         // query positions per wave
             constexpr int QP = kAttWaves * PW; // per block
             // K and V tiles, two buffers each.  Tile t's P V product is issued in
             // step t + 1, beside the softmax of tile t + 1, so V(t) stays resident
@@ -189,247 +481,51 @@ namespace q3k
             const bool wave_partial = wave_s0 + PW > S;
 
             bf16x8_t qf[kAttD / 16];
-            {
-                const Vec8 *qrow = reinterpret_cast<const Vec8 *>(a.q + ((b * S + s_col) * a.Hq + h_col) * kAttD);
-                const Vec8 zero = {{0u, 0u, 0u, 0u}};
-#pragma unroll
-                for (int c = 0; c < kAttD / 16; ++c)
-                    qf[c] = as_bf8(col_ok ? qrow[2 * c + lg] : zero);
-            }
-
-            const uint16_t *kbase = a.k + b * a.ks0 + kvh * a.ks2;
-            const uint16_t *vbase = a.v + b * a.vs0 + kvh * a.vs2;
-            // staging: wave w fills rows kStageRows w .. + kStageRows - 1 of a K
-            // (or V) buffer, kRowsPerLoad rows per load; lane j lands in slot
-            // j % 16 of row j / 16 and so fetches the chunk that slot holds.
-            // A tile's loads address from a buffer resource based at its first
-            // key, so the per-lane byte offsets stay fixed (32-bit: checked by
-            // the launcher).  Rows past the causal range repeat the last key
-            // (finite data, later masked or weighted by zero).
-            const int st_row = kStageRows * wave + lane / 16, st_slot = lane % 16;
-            const int32_t kstride = static_cast<int32_t>(a.ks1) * 2, vstride = static_cast<int32_t>(a.vs1) * 2;
-            int32_t k_voff[kStageRows / kRowsPerLoad], v_voff[kStageRows / kRowsPerLoad];
-#pragma unroll
-            for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
-            {
-                const int r = st_row + kRowsPerLoad * x;
-                k_voff[x] = r * kstride + 16 * k_slot(r, st_slot);
-                v_voff[x] = r * vstride + 16 * v_slot(r, st_slot);
-            }
-            auto issue_rows = [&](int tile, unsigned char *buf, const uint16_t *base, int64_t row_stride,
-                                  int32_t byte_stride, const int32_t *voff, auto slot) {
-                const int32_t key0 = tile * kKeyTile;
-                const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + static_cast<int64_t>(key0) * row_stride);
-                unsigned char *dst = buf + kStageRows * wave * kRowBytes;
-                if (key0 + kKeyTile <= n_keys)
-                {
-#pragma unroll
-                    for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
-                        dma16(rs, voff[x], dst + kRowsPerLoad * x * kRowBytes);
-                }
-                else
-                {
-                    const int last = n_keys - 1 - key0;
-#pragma unroll
-                    for (int x = 0; x < kStageRows / kRowsPerLoad; ++x)
-                    {
-                        const int r = st_row + kRowsPerLoad * x;
-                        const int rr = r < last ? r : last;
-                        dma16(rs, rr * byte_stride + 16 * slot(r, st_slot), dst + kRowsPerLoad * x * kRowBytes);
-                    }
-                }
-            };
-            auto issue_k = [&](int tile, unsigned char *buf) {
-                issue_rows(tile, buf, kbase, a.ks1, kstride, k_voff, [](int r, int c) { return k_slot(r, c); });
-            };
-            auto issue_v = [&](int tile, unsigned char *buf) {
-                issue_rows(tile, buf, vbase, a.vs1, vstride, v_voff, [](int r, int c) { return v_slot(r, c); });
-            };
-            // per-lane LDS byte offsets of the fragments: K rows li (+ 32 hh),
-            // chunk 2 c + lg, two 8-byte halves; V transpose reads: the lanes of
-            // each 16 give rows 4 lg + j / 4 (+ 8 per 8-key step) and 4 dims
-            // 32 dt + 16 ((lane / 16) % 2) + 4 (j % 4) .. + 3, and each lane gets
-            // 4 consecutive keys of one dim (dim 32 dt + li)
-            const int tj = lane % 16;
-            const int v_row = 4 * lg + tj / 4;
+            load_q(a, b, s_col, h_col, col_ok, lg, qf);
+            Q3K_ATTN_STAGING(kAttWaves)
             int v_off[kAttD / 32];
-#pragma unroll
-            for (int dt = 0; dt < kAttD / 32; ++dt)
-                v_off[dt] = v_row * kRowBytes + 16 * v_slot(v_row, 4 * dt + 2 * ((lane / 16) % 2) + (tj % 4) / 2) +
-                            8 * (tj % 2);
+            v_offsets(lane, v_off);
             f32x16_t o[kAttD / 32];
 #pragma unroll
             for (int dt = 0; dt < kAttD / 32; ++dt)
                 o[dt] = f32x16_t{};
             float m = -__builtin_huge_valf(), l = 0.0f;
             const float scale2 = a.scale * kLog2e;
-
-            // O^T += V^T P^T for one tile: step i covers the 16-key chunk i / 4
-            // (hh = i / 8, mm = (i / 4) % 2) and dims 32 (i % 4) .. + 31.  The
-            // transpose reads run kAhead steps ahead of the MFMAs that use them.
-            auto read_v = [&](const unsigned char *v_lds, int i) {
-                // keys 16 (i / 4) + 8 t + 4 lg + 0..3 in elements 4 t .. 4 t + 3:
-                // the keys of the P^T elements this lane holds
-                const unsigned char *vp = v_lds + v_off[i % 4] + 16 * (i / 4) * kRowBytes;
-                const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp));
-                const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(vp + 8 * kRowBytes));
-                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-            };
             bf16x8_t phi[2][2], plo[2][2]; // P of the tile whose P V is still to be issued
-            auto pv = [&](const unsigned char *v_lds) {
-                bf16x8_t vq[kAhead + 1];
-#pragma unroll
-                for (int i = 0; i < kAhead; ++i)
-                    vq[i] = read_v(v_lds, i);
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                {
-                    if (i + kAhead < 16)
-                        vq[(i + kAhead) % (kAhead + 1)] = read_v(v_lds, i + kAhead);
-                    const int dt = i % 4, hh = i / 8, mm = (i / 4) % 2;
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], phi[hh][mm], o[dt], 0, 0, 0);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vq[i % (kAhead + 1)], plo[hh][mm], o[dt], 0, 0, 0);
-                }
-            };
 
             // One step: load K(tile + 1); S^T = K(tile) Q^T; the P V of the
-            // previous tile (WITH_PV) interleaved with this tile's softmax; after
-            // the barrier, load V(tile + 1) into v_prev.
+            // previous tile (WITH_PV); this tile's softmax; after the barrier,
+            // load V(tile + 1) into v_prev.
             auto step = [&](auto with_pv, int tile, const unsigned char *k_cur, unsigned char *k_next,
-                            unsigned char *v_prev) {
+                            unsigned char *v_prev) __attribute__((always_inline)) {
                 if (tile + 1 < ntiles)
-                    issue_k(tile + 1, k_next); // in flight while this tile is computed
-                const unsigned char *k_lds = k_cur;
+                    load_k(tile + 1, k_next); // in flight while this tile is computed
                 if (wave_active)
                 {
                     const int32_t key0 = tile * kKeyTile;
-                    auto read_k = [&](int c, int hh) {
-                        return *reinterpret_cast<const Vec8 *>(k_lds + (32 * hh + li) * kRowBytes +
-                                                               16 * k_slot(li, 2 * c + lg));
-                    };
-                    f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
-                    Vec8 kq[kAhead + 1][2];
-#pragma unroll
-                    for (int c = 0; c < kAhead; ++c)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh)
-                            kq[c][hh] = read_k(c, hh);
-#pragma unroll
-                    for (int c = 0; c < kAttD / 16; ++c)
-                    {
-                        if (c + kAhead < kAttD / 16)
-#pragma unroll
-                            for (int hh = 0; hh < 2; ++hh)
-                                kq[(c + kAhead) % (kAhead + 1)][hh] = read_k(c + kAhead, hh);
-                        __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of these MFMAs
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh)
-                            sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kq[c % (kAhead + 1)][hh]), qf[c],
-                                                                               sacc[hh], 0, 0, 0);
-                    }
-
-                    // Masked scores become -inf before the max; the max of the raw
-                    // scores times the (positive) scale is the max of the scaled ones.
+                    f32x16_t sacc[2];
+                    qk_tile(k_cur, qf, li, lg, sacc);
                     if (key0 + kKeyTile - 1 > start + wave_s0 || wave_partial)
-                    {
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                            {
-                                const int32_t kk = key0 + 32 * hh + 8 * (r / 4) + 4 * lg + (r % 4);
-                                if (kk > last_key || !col_ok)
-                                    sacc[hh][r] = -__builtin_huge_valf();
-                            }
-                    }
+                        mask_tile(sacc, key0, lg, last_key, col_ok);
                     if constexpr (decltype(with_pv)::value)
-                        pv(v_prev); // the previous tile's P V, independent of the softmax below
-                    float mloc = sacc[0][0];
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            mloc = fmaxf(mloc, sacc[hh][r]);
-                    mloc = pair_max(mloc);
-                    // The weights are taken relative to a reference m that moves
-                    // only when a tile's max exceeds it by more than kLazyMax
-                    // (log2 units): the weights stay below 2^kLazyMax, and the
-                    // rescale of o (alpha != 1) is left for the rare tiles that
-                    // move it.  An all-masked column keeps m = -inf and weight 0.
-                    const float m_tile = mloc * scale2;
-                    const bool move = m_tile > m + kLazyMax;
-                    const float m_new = move ? m_tile : m;
-                    const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
-                    const float alpha = move ? __builtin_amdgcn_exp2f(m - m_use) : 1.0f;
-                    float psum = 0.0f;
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                        for (int mm = 0; mm < 2; ++mm)
-                        {
-                            Vec8 h8, l8;
-#pragma unroll
-                            for (int j = 0; j < 4; ++j)
-                            {
-                                const float x0 = __builtin_amdgcn_exp2f(
-                                    __builtin_fmaf(sacc[hh][8 * mm + 2 * j], scale2, -m_use));
-                                const float x1 = __builtin_amdgcn_exp2f(
-                                    __builtin_fmaf(sacc[hh][8 * mm + 2 * j + 1], scale2, -m_use));
-                                psum += x0;
-                                psum += x1;
-                                const uint32_t hp = pack_rne(x0, x1);
-                                h8.d[j] = hp;
-                                l8.d[j] = pack_rne(x0 - bf_lo(hp), x1 - bf_hi(hp));
-                            }
-                            phi[hh][mm] = as_bf8(h8);
-                            plo[hh][mm] = as_bf8(l8);
-                        }
-                    psum = pair_sum(psum);
-                    l = l * alpha + psum;
-                    m = m_new;
-                    if constexpr (decltype(with_pv)::value)
-                    {
-                        // interleave MFMA and softmax VALU work in turn, so the matrix
-                        // pipe runs under the softmax.  The transpose reads keep their
-                        // distance: the first kAhead steps' reads lead, and each step's
-                        // two reads (for step i + kAhead) follow its MFMAs.
-                        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0); // DS reads
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                        {
-                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-                            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); // VALU
-                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-                            if (i + kAhead < 16)
-                                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                        }
-                    }
-                    // o now holds the tiles before this one at the previous reference;
-                    // it rarely moves after the first tile, and multiplying by
-                    // alpha == 1 changes nothing, so the wave skips it then
-                    if (__any(alpha != 1.0f))
-                    {
-#pragma unroll
-                        for (int dt = 0; dt < kAttD / 32; ++dt)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                o[dt][r] *= alpha;
-                    }
+                        pv_tile(v_prev, v_off, phi, plo, o);
+                    const float alpha = softmax_tile(sacc, scale2, m, l, phi, plo);
+                    // o holds the tiles before this one at the previous reference
+                    rescale(o, alpha);
                 }
                 // this wave's loads of K(tile + 1) and V(tile) have landed; after the
                 // barrier all have, and every wave is done with K(tile) and V(tile - 1)
                 __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
                 if (tile + 1 < ntiles)
-                    issue_v(tile + 1, v_prev);
+                    load_v(tile + 1, v_prev);
             };
             using no_pv = std::integral_constant<bool, false>;
             using with_pv = std::integral_constant<bool, true>;
             if (tile_begin < ntiles)
             {
-                issue_k(tile_begin, k_a);
-                issue_v(tile_begin, v_a);
+                load_k(tile_begin, k_a);
+                load_v(tile_begin, v_a);
                 __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
                 // V(t) sits in v_a when t - tile_begin is even, else in v_b
@@ -443,46 +539,13 @@ namespace q3k
                 if (wave_active)
                 {
                     if ((ntiles - 1 - tile_begin) % 2 == 0)
-                        pv(v_a);
+                        pv_tile(v_a, v_off, phi, plo, o);
                     else
-                        pv(v_b);
+                        pv_tile(v_b, v_off, phi, plo, o);
                 }
             }
-
-            if (!col_ok)
-                return;
-            if (a.splits > 1)
-            {
-                const int64_t slot = static_cast<int64_t>(sp) * a.rows + (b * S + s_col) * a.Hq + h_col;
-                float *po = a.part_o + slot * kAttD;
-#pragma unroll
-                for (int dt = 0; dt < kAttD / 32; ++dt)
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4)
-                    {
-                        const float4 w = {o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-                        *reinterpret_cast<float4 *>(po + dt * 32 + 8 * q4 + 4 * lg) = w;
-                    }
-                if (lg == 0)
-                {
-                    a.part_ml[2 * slot] = m;
-                    a.part_ml[2 * slot + 1] = l;
-                }
-                return;
-            }
-            const float inv = 1.0f / l;
-            uint16_t *orow = a.out + ((b * S + s_col) * a.Hq + h_col) * kAttD;
-#pragma unroll
-            for (int dt = 0; dt < kAttD / 32; ++dt)
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4)
-                {
-                    const int d = dt * 32 + 8 * q4 + 4 * lg;
-                    uint2 w;
-                    w.x = pack_rne(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv);
-                    w.y = pack_rne(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
-                    *reinterpret_cast<uint2 *>(orow + d) = w;
-                }
+            if (col_ok)
+                store_column(a, sp, b, s_col, h_col, lg, o, m, l);
         }
 
         // Merges the key slices of one query row per wave: weights

@@ -530,6 +530,13 @@ def test_attention_kat(q3k, hip, oracle):
     (2, 21, 4, 8, 2, 64, 32, 0),        # head_dim 64: generic kernel
     (1, 12, 3, 8, 2, 128, 16, 2),       # unaligned caches: generic kernel
     (1, 6, 0, 4, 4, 256, 6, 0),         # head_dim 256: generic kernel
+    # prefill blocks of two wave groups (S >= 256 / G), partial last blocks
+    (1, 300, 20, 8, 8, 128, 330, 0),    # G = 1
+    (2, 130, 0, 16, 8, 128, 140, 0),    # G = 2
+    (1, 100, 9, 32, 8, 128, 120, 0),    # G = 4, the second group partly empty
+    (1, 45, 7, 64, 8, 128, 60, 0),      # G = 8
+    (1, 20, 3, 32, 2, 128, 30, 0),      # G = 16
+    (1, 9, 60, 32, 1, 128, 70, 0),      # G = 32
 ])
 def test_gqa_attention(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, D, cap, offset):
     name = f"gqa_attention B={B} S={S} start={start} Hq={Hq} Hkv={Hkv} D={D} cap={cap} offset={offset}"
