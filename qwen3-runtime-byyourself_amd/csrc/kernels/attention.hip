@@ -53,7 +53,6 @@ namespace q3k
         constexpr int kKeyTile = 64;                          // keys per pipeline step
         constexpr int kRowBytes = kAttD * 2;                  // one K or V row in LDS
         constexpr int kHalfBytes = kKeyTile * kRowBytes;      // the K (or V) rows of a tile
-        constexpr int kTileBytes = 2 * kHalfBytes;            // K rows, then V rows
         constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
         constexpr int kAhead = 2;                             // LDS fragment reads in flight ahead of use
         constexpr float kLazyMax = 8.0f;                      // log2 headroom before the softmax reference moves
