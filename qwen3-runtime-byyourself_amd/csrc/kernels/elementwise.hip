@@ -26,6 +26,8 @@ namespace q3k
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
         constexpr int kNtmCopy = 3;
+        // Below this many blocks at the unrolled shape a launch leaves CUs idle.
+        constexpr int64_t kSmallLaunchBlocks = 1024;
 
         // exp(x) for the SiLU denominator: Cody-Waite style split of
         // x * log2(e) into an integer and a fraction, the fraction through the
@@ -194,8 +196,19 @@ namespace q3k
             const int64_t blocks = (nvec + kVecPerBlock - 1) / kVecPerBlock;
             if (aligned16(a) && aligned16(b) && aligned16(out) && blocks < (int64_t{1} << 31))
             {
-                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
-                    a, b, out, nvec, n);
+                if (U > 1 && blocks < kSmallLaunchBlocks)
+                {
+                    // Few tokens (decode): one vector per thread puts U times
+                    // as many blocks on the CUs and halves each wave's chain.
+                    const int64_t b1 = (nvec + kBlock - 1) / kBlock;
+                    binary_vec_kernel<OP, 1, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(b1 > 0 ? b1 : 1)), dim3(kBlock), 0, stream>>>(
+                        a, b, out, nvec, n);
+                }
+                else
+                {
+                    binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
+                        a, b, out, nvec, n);
+                }
             }
             else
             {

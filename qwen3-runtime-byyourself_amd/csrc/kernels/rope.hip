@@ -335,6 +335,7 @@ namespace q3k
         // Heads per lane: 4 when the head count allows it (32 or 64 query
         // heads), else 2 (8 KV heads), else 1.
         int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
+        constexpr int64_t kSmallLaunchHeads = 16384; // below this many (token, head) rows: one head per lane group
 
         template <bool NORM, bool KV, int HGQ, int HGK>
         void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
@@ -352,8 +353,12 @@ namespace q3k
         void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
                           int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream, const KvDest &kv = {})
         {
-            const int gq = heads_per_lane(hq);
-            const int gk = k == nullptr ? gq : heads_per_lane(hk);
+            // A small launch (decode: a few tokens) spreads one head per lane
+            // group over more waves: fewer heads per wave shorten its serial
+            // chain, and the waves fill more CUs.
+            const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kSmallLaunchHeads;
+            const int gq = small ? 1 : heads_per_lane(hq);
+            const int gk = small ? 1 : (k == nullptr ? gq : heads_per_lane(hk));
             const int key = gq * 10 + gk;
             switch (key)
             {
