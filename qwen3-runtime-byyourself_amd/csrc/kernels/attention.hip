@@ -547,34 +547,69 @@ namespace q3k
                 store_column(a, sp, b, s_col, h_col, lg, o, m, l);
         }
 
-        // Merges the key slices of one query row per wave: weights
-        // 2^(m_s - max m) (the reference maxima are in the log2 domain), then
-        // sum_s w_s O_s / sum_s w_s l_s; lane t holds dims 2t, 2t + 1.
-        __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *__restrict__ part_o,
-                                                                      const float *__restrict__ part_ml,
-                                                                      uint16_t *__restrict__ out, int64_t rows,
-                                                                      int32_t splits)
+        // Merges the key slices of one query row per block of four waves
+        // (splits <= kMaxSplits).  Every load is issued before any is used:
+        // lane s of each wave reads slice s's reference max and sum, and wave
+        // w the unnormalised O^T of slices w, w + 4, ...  Weights
+        // 2^(m_s - max m) (the maxima are in the log2 domain), then
+        // sum_s w_s O_s / sum_s w_s l_s; lane t holds dims 2t, 2t + 1, and the
+        // four waves' partial sums meet in LDS.
+        constexpr int kMaxSplits = 64;
+        constexpr int kCombineWaves = 4;
+        constexpr int kSplitsPerWave = kMaxSplits / kCombineWaves;
+
+        __global__ __launch_bounds__(kCombineWaves * kWave) void attn_combine_kernel(const float *__restrict__ part_o,
+                                                                                      const float *__restrict__ part_ml,
+                                                                                      uint16_t *__restrict__ out,
+                                                                                      int64_t rows, int32_t splits)
         {
-            const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) +
-                                __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-            if (row >= rows)
-                return;
+            __shared__ float2 wave_acc[kCombineWaves][kWave];
+            const int64_t row = blockIdx.x;
+            const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             const int lane = threadIdx.x % kWave;
-            float mx = -__builtin_huge_valf();
-            for (int sp = 0; sp < splits; ++sp)
-                mx = fmaxf(mx, part_ml[2 * (static_cast<int64_t>(sp) * rows + row)]);
-            float lsum = 0.0f, a0 = 0.0f, a1 = 0.0f;
-            for (int sp = 0; sp < splits; ++sp)
+            float2 ml = make_float2(-__builtin_huge_valf(), 0.0f);
+            if (lane < splits)
+                ml = reinterpret_cast<const float2 *>(part_ml)[static_cast<int64_t>(lane) * rows + row];
+            float2 v[kSplitsPerWave];
+#pragma unroll
+            for (int u = 0; u < kSplitsPerWave; ++u)
             {
-                const int64_t slot = static_cast<int64_t>(sp) * rows + row;
-                const float w = __builtin_amdgcn_exp2f(part_ml[2 * slot] - mx);
-                lsum += w * part_ml[2 * slot + 1];
-                const float2 v = reinterpret_cast<const float2 *>(part_o + slot * kAttD)[lane];
-                a0 += w * v.x;
-                a1 += w * v.y;
+                const int sp = wave + kCombineWaves * u;
+                if (sp < splits)
+                    v[u] = reinterpret_cast<const float2 *>(part_o + (static_cast<int64_t>(sp) * rows + row) * kAttD)[lane];
             }
-            const float inv = 1.0f / lsum;
-            reinterpret_cast<uint32_t *>(out + row * kAttD)[lane] = pack_rne(a0 * inv, a1 * inv);
+            float mx = ml.x;
+#pragma unroll
+            for (int off = kWave / 2; off > 0; off /= 2)
+                mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+            const float w = lane < splits ? __builtin_amdgcn_exp2f(ml.x - mx) : 0.0f;
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < kSplitsPerWave; ++u)
+            {
+                const int sp = wave + kCombineWaves * u;
+                if (sp < splits)
+                {
+                    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
+                    a0 += ws * v[u].x;
+                    a1 += ws * v[u].y;
+                }
+            }
+            wave_acc[wave][lane] = make_float2(a0, a1);
+            const float lsum = group_sum<kWave>(w * ml.y);
+            __syncthreads();
+            if (wave == 0)
+            {
+                float2 t = wave_acc[0][lane];
+#pragma unroll
+                for (int k = 1; k < kCombineWaves; ++k)
+                {
+                    t.x += wave_acc[k][lane].x;
+                    t.y += wave_acc[k][lane].y;
+                }
+                const float inv = 1.0f / lsum;
+                reinterpret_cast<uint32_t *>(out + row * kAttD)[lane] = pack_rne(t.x * inv, t.y * inv);
+            }
         }
 
         // Generic path: one wave per query row (b, s, h); lane t holds head
@@ -672,8 +707,8 @@ namespace q3k
             const int64_t most = cached / kMinSplitKeys;
             if (want > most)
                 want = most;
-            if (want > 64)
-                want = 64;
+            if (want > kMaxSplits)
+                want = kMaxSplits;
             if (want < 2)
                 return p;
             int64_t keys = (cached + want - 1) / want;
@@ -694,7 +729,7 @@ namespace q3k
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
             attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kAttBlock), 0, stream>>>(a);
             if (a.splits > 1)
-                attn_combine_kernel<<<dim3(static_cast<unsigned>((a.rows + 3) / 4)), dim3(kBlock), 0, stream>>>(
+                attn_combine_kernel<<<dim3(static_cast<unsigned>(a.rows)), dim3(kCombineWaves * kWave), 0, stream>>>(
                     a.part_o, a.part_ml, a.out, a.rows, a.splits);
         }
     } // namespace
@@ -762,7 +797,8 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
     if (mfma_ok(a, G))
     {
         const SplitPlan plan = plan_split(B, S, Hq, Hkv, cached);
-        if (plan.splits > 1 && workspace != nullptr && workspace_bytes >= plan.bytes && aligned16(workspace))
+        if (plan.splits > 1 && plan.splits <= kMaxSplits && workspace != nullptr && workspace_bytes >= plan.bytes &&
+            aligned16(workspace))
         {
             a.splits = plan.splits;
             a.split_keys = plan.split_keys;
