@@ -205,14 +205,26 @@ Q3K_API int64_t q3k_gqa_attention_workspace_bytes(int64_t B, int64_t S,
  * Argmax over the last dimension: out[r] = index of the largest of
  * x[r * row_stride + 0 .. search_size - 1] (bf16), NaN counted as -inf, ties
  * to the smaller index; int32 out [rows].  search_size in [1, row_stride]
- * (a valid vocabulary prefix of padded logits).  Bit-exact.
+ * (a valid vocabulary prefix of padded logits).  Bit-exact.  workspace
+ * (8-byte aligned device memory, may be NULL) of at least
+ * q3k_argmax_workspace_bytes(rows, search_size) bytes lets a launch with
+ * few rows cut each row into slices searched by separate blocks; the result
+ * is the same either way.  Calls that share a workspace must not overlap.
  * Replaces qwen3::ops::argmax_last_dimension, src/ops/argmax.cu:163-214
  * (kernel :34-100), the greedy path of Sampler::sample
  * (src/generation/sampler.cpp:288-291).
  */
 Q3K_API int q3k_argmax_bf16(const uint16_t *x, int32_t *out, int64_t rows,
                   int64_t row_stride, int64_t search_size,
+                  void *workspace, int64_t workspace_bytes,
                   q3k_stream_t stream);
+
+/*
+ * Workspace bytes q3k_argmax_bf16 would use to slice these rows (0: it does
+ * not slice).  No counterpart in the reference (its kernel is one block per
+ * row).
+ */
+Q3K_API int64_t q3k_argmax_workspace_bytes(int64_t rows, int64_t search_size);
 
 /*
  * Top-k candidates of sampling.  For each row r of logits (bf16, row_stride
@@ -231,7 +243,17 @@ Q3K_API int q3k_topk_candidates_bf16(const uint16_t *logits, int64_t rows,
                           int64_t row_stride, int64_t search_size, int32_t k,
                           int32_t cap, int32_t *count, int32_t *cand_index,
                           uint16_t *cand_logit, int32_t *nonfinite,
+                          void *workspace, int64_t workspace_bytes,
                           q3k_stream_t stream);
+
+/*
+ * Workspace bytes q3k_topk_candidates_bf16 would use to cut these rows into
+ * slices searched by separate blocks (0: it does not); the workspace (16-byte
+ * aligned device memory, may be NULL) changes the speed, not the result, and
+ * calls that share one must not overlap.  No counterpart in the reference
+ * (its selection runs on the host).
+ */
+Q3K_API int64_t q3k_topk_workspace_bytes(int64_t rows, int64_t search_size, int32_t k);
 
 /*
  * KV-cache append: K and V [B, S, row_bytes] (contiguous) are copied to rows

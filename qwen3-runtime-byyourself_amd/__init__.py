@@ -82,8 +82,10 @@ SIGNATURES = {
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
     "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p, _i64, _p],
     "q3k_gqa_attention_workspace_bytes": [_i64, _i64, _i32, _i32, _i32, _i64],
-    "q3k_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p],
-    "q3k_topk_candidates_bf16": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p],
+    "q3k_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "q3k_argmax_workspace_bytes": [_i64, _i64],
+    "q3k_topk_candidates_bf16": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _i64, _p],
+    "q3k_topk_workspace_bytes": [_i64, _i64, _i32],
     "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "q3k_qk_norm_rope_kv_append_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p,
                                         _p, _p, _i64, _i64, _p],
@@ -202,14 +204,24 @@ def gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, cached):
     return int(load().q3k_gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, cached))
 
 
-def argmax(x, out, rows, row_stride, search_size, stream=None):
-    _check(load().q3k_argmax_bf16(_ptr(x), _ptr(out), rows, row_stride, search_size, _ptr(stream)))
+def argmax(x, out, rows, row_stride, search_size, stream=None, workspace=None, workspace_bytes=0):
+    _check(load().q3k_argmax_bf16(_ptr(x), _ptr(out), rows, row_stride, search_size, _ptr(workspace),
+                                  workspace_bytes, _ptr(stream)))
+
+
+def argmax_workspace_bytes(rows, search_size):
+    return int(load().q3k_argmax_workspace_bytes(rows, search_size))
 
 
 def topk_candidates(logits, rows, row_stride, search_size, k, cap, count, cand_index, cand_logit, nonfinite,
-                    stream=None):
+                    stream=None, workspace=None, workspace_bytes=0):
     _check(load().q3k_topk_candidates_bf16(_ptr(logits), rows, row_stride, search_size, k, cap, _ptr(count),
-                                           _ptr(cand_index), _ptr(cand_logit), _ptr(nonfinite), _ptr(stream)))
+                                           _ptr(cand_index), _ptr(cand_logit), _ptr(nonfinite), _ptr(workspace),
+                                           workspace_bytes, _ptr(stream)))
+
+
+def topk_workspace_bytes(rows, search_size, k):
+    return int(load().q3k_topk_workspace_bytes(rows, search_size, k))
 
 
 def kv_append(k, v, k_cache, v_cache, B, S, row_bytes, seq_cap, start, stream=None):

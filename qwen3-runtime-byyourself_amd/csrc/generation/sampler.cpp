@@ -193,12 +193,16 @@ namespace qwen3::generation
             Tensor bad = Tensor::empty(Shape{batch}, DType::Int32, logits.device());
             Tensor index = Tensor::empty(Shape{batch, cap}, DType::Int32, logits.device());
             Tensor value = Tensor::empty(Shape{batch, cap}, DType::BFloat16, logits.device());
+            // few rows are cut into slices searched by separate blocks; their lists need a workspace
+            const std::int64_t ws_bytes = q3k_topk_workspace_bytes(batch, valid, config_.top_k);
+            Tensor workspace = Tensor::empty(Shape{(ws_bytes + 3) / 4}, DType::Int32, logits.device());
             ops::detail::launch_on(logits.device(), [&](q3k_stream_t stream) {
                 return q3k_topk_candidates_bf16(static_cast<const uint16_t *>(logits.data()), batch, vocab, valid,
                                                 config_.top_k, cap, static_cast<int32_t *>(count.data()),
                                                 static_cast<int32_t *>(index.data()),
                                                 static_cast<uint16_t *>(value.data()),
-                                                static_cast<int32_t *>(bad.data()), stream);
+                                                static_cast<int32_t *>(bad.data()),
+                                                ws_bytes > 0 ? workspace.data() : nullptr, ws_bytes, stream);
             });
             const auto counts = to_host<std::int32_t>(count);
             const auto flags = to_host<std::int32_t>(bad);

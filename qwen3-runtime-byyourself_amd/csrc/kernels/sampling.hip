@@ -24,6 +24,13 @@
 // of a row share few exponents, so most increments hit a handful of bins and
 // each wave counts into its own histogram.  A row with a non-finite logit is
 // flagged (the reference throws for it).
+//
+// With few rows and a caller workspace, each row is cut into slices: one
+// block per (row, slice) finds the slice's bound and lists its logits at or
+// above it (steps 1-2 on the slice), and one block per row keeps the listed
+// logits at or above the largest slice bound and finishes with step 3 (or
+// the whole-row select when a slice saw a non-finite logit or its list
+// overflowed).  The candidate set is the same either way.
 #include "q3k_common.hpp"
 
 namespace q3k
@@ -49,21 +56,45 @@ namespace q3k
             return (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu);
         }
 
-        // the bin holding the k-th largest key, counting down from bin 255, and
-        // the rank of that key inside the bin (single thread; 256 bins)
+        // The bin holding the k-th largest key, counting down from bin 255, and
+        // the rank of that key inside the bin (bin 0 when bins 255 .. 1 hold
+        // fewer than k keys).  Called by every lane of one wave: lane l holds
+        // bins 255 - 4l .. 252 - 4l, a prefix sum over the lanes gives the
+        // keys above each lane's bins, and the first lane whose bins reach k
+        // walks its four bins and writes the result.
         __device__ __forceinline__ void find_bin(const uint32_t *hist, uint32_t k, uint32_t *bin_out,
                                                  uint32_t *rank_out)
         {
-            uint32_t above = 0;
-            int bin = 255;
-            for (; bin > 0; --bin)
+            const int lane = threadIdx.x % kWave;
+            const int top = 255 - 4 * lane;
+            uint32_t c[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                c[j] = hist[top - j];
+            const uint32_t local = c[0] + c[1] + c[2] + c[3];
+            uint32_t incl = local;
+#pragma unroll
+            for (int off = 1; off < kWave; off *= 2)
             {
-                if (above + hist[bin] >= k)
-                    break;
-                above += hist[bin];
+                const uint32_t v = __shfl_up(incl, off, kWave);
+                if (lane >= off)
+                    incl += v;
             }
-            *bin_out = static_cast<uint32_t>(bin);
-            *rank_out = k - above;
+            const uint64_t hit = __ballot(incl >= k);
+            const int owner = hit == 0 ? kWave - 1 : __ffsll(static_cast<unsigned long long>(hit)) - 1;
+            if (lane == owner)
+            {
+                uint32_t above = incl - local;
+                int j = 0;
+                for (; j < 3; ++j)
+                {
+                    if (above + c[j] >= k)
+                        break;
+                    above += c[j];
+                }
+                *bin_out = static_cast<uint32_t>(top - j);
+                *rank_out = k - above;
+            }
         }
 
         // k-th largest (1 <= k <= n) of the 16-bit keys key_at(0 .. n - 1),
@@ -78,7 +109,7 @@ namespace q3k
             for (int i = tid; i < n; i += kSelBlock)
                 atomicAdd(&hist[key_at(i) >> 8], 1u);
             __syncthreads();
-            if (tid == 0)
+            if (tid < kWave)
                 find_bin(hist, k, &sel[0], &sel[1]);
             __syncthreads();
             const uint32_t hi = sel[0], rank = sel[1];
@@ -92,219 +123,430 @@ namespace q3k
                     atomicAdd(&hist[key & 255u], 1u);
             }
             __syncthreads();
-            if (tid == 0)
+            if (tid < kWave)
             {
-                uint32_t lo, unused;
-                find_bin(hist, rank, &lo, &unused);
-                sel[2] = (hi << 8) | lo;
+                uint32_t unused;
+                find_bin(hist, rank, &sel[2], &unused);   // the low byte
             }
+            __syncthreads();
+            if (tid == 0)
+                sel[2] = (hi << 8) | sel[2];
             __syncthreads();
             return sel[2];
         }
 
         __device__ __forceinline__ float bf_val(uint32_t b) { return __uint_as_float(b << 16); }
 
-        // Visits logits c = 0 .. n - 1 of a row, each thread its share:
+        // Visits logits c = begin .. end - 1 of a row, each thread its share:
         // 16-byte chunks (chunk j to thread j % kSelBlock) when the row is
-        // 16-byte aligned, kSelUnroll chunks loaded before any is visited (one
-        // block per row: its loads in flight set the row's read rate); single
-        // logits otherwise.  f(c, bits).
+        // 16-byte aligned (begin is then a multiple of 8), kSelUnroll chunks
+        // loaded before any is visited (one block per row or slice: its loads
+        // in flight set the read rate); single logits otherwise.  f(c, bits).
         constexpr int kSelUnroll = 4;
         template <typename F>
-        __device__ __forceinline__ void for_row(const uint16_t *r, int64_t n, F f)
+        __device__ __forceinline__ void for_row(const uint16_t *r, int64_t begin, int64_t end, F f)
         {
             const int tid = threadIdx.x;
             if ((reinterpret_cast<uintptr_t>(r) & 15u) == 0)
             {
-                const int64_t chunks = n / 8;
+                const int64_t chunk_end = end / 8;
                 const Vec8 *rv = reinterpret_cast<const Vec8 *>(r);
-                auto visit = [&](int64_t j, const Vec8 &v) {
+                auto visit = [&](int64_t j, const Vec8 &v) __attribute__((always_inline)) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         f(8 * j + e, (e % 2 == 0) ? (v.d[e / 2] & 0xffffu) : (v.d[e / 2] >> 16));
                 };
-                int64_t j = tid;
-                for (; j + (kSelUnroll - 1) * kSelBlock < chunks; j += kSelUnroll * kSelBlock)
+                // groups of kSelUnroll chunks, the last one partial: a
+                // thread's loads of a group are all issued before any visit
+                for (int64_t j = begin / 8 + tid; j < chunk_end; j += kSelUnroll * kSelBlock)
                 {
                     Vec8 v[kSelUnroll];
 #pragma unroll
                     for (int u = 0; u < kSelUnroll; ++u)
-                        v[u] = load8<false>(rv + j + u * kSelBlock);
+                        if (j + u * kSelBlock < chunk_end)
+                            v[u] = load8<false>(rv + j + u * kSelBlock);
 #pragma unroll
                     for (int u = 0; u < kSelUnroll; ++u)
-                        visit(j + u * kSelBlock, v[u]);
+                        if (j + u * kSelBlock < chunk_end)
+                            visit(j + u * kSelBlock, v[u]);
                 }
-                for (; j < chunks; j += kSelBlock)
-                    visit(j, load8<false>(rv + j));
-                for (int64_t c = 8 * chunks + tid; c < n; c += kSelBlock)
+                const int64_t tail = 8 * chunk_end > begin ? 8 * chunk_end : begin;
+                for (int64_t c = tail + tid; c < end; c += kSelBlock)
                     f(c, static_cast<uint32_t>(r[c]));
             }
             else
             {
-                for (int64_t c = tid; c < n; c += kSelBlock)
+                for (int64_t c = begin + tid; c < end; c += kSelBlock)
                     f(c, static_cast<uint32_t>(r[c]));
             }
         }
 
+        // LDS of one selection block.
+        struct SelShared
+        {
+            uint32_t wave_hist[kSelWaves][256];
+            uint32_t hist[256];
+            uint32_t thread_max[kSelBlock];
+            uint32_t list_bits[kCandMax];
+            int32_t list_index[kCandMax];
+            uint32_t sel[3];
+            uint32_t found, bad, listed, bound, overflow;
+        };
+
+        // Where a row's candidates go.
+        struct CandOut
+        {
+            int32_t cap;
+            int32_t *cand_index;
+            uint16_t *cand_logit;
+        };
+
+        // Each thread's largest logit of [begin, end) as a key in thread_max
+        // (a thread without logits counts as key 0, below every finite key),
+        // and the non-finite flag in sh.bad; ends with a barrier.
+        __device__ __forceinline__ void thread_maxima(const uint16_t *r, int64_t begin, int64_t end, SelShared &sh)
+        {
+            float tmax = -__builtin_huge_valf();
+            uint32_t my_bad = 0u;
+            for_row(r, begin, end, [&](int64_t, uint32_t b) __attribute__((always_inline)) {
+                my_bad |= (b & 0x7f80u) == 0x7f80u ? 1u : 0u;
+                tmax = fmaxf(tmax, bf_val(b));
+            });
+            sh.thread_max[threadIdx.x] = tmax == -__builtin_huge_valf() ? 0u : sel_key(__float_as_uint(tmax) >> 16);
+            if (my_bad)
+                atomicOr(&sh.bad, 1u);
+            __syncthreads();
+        }
+
+        // Appends (bits, index) to the LDS list when `take`: one LDS atomic per
+        // wave, slots by lane rank; entries past kCandMax are counted, not kept.
+        __device__ __forceinline__ void list_append(SelShared &sh, bool take, uint32_t b, int32_t index)
+        {
+            const uint64_t ballot = __ballot(take);
+            if (ballot == 0)
+                return;
+            const int lane = threadIdx.x % kWave;
+            const int leader = __ffsll(static_cast<unsigned long long>(ballot)) - 1;
+            uint32_t base = 0u;
+            if (lane == leader)
+                base = atomicAdd(&sh.listed, static_cast<uint32_t>(__popcll(ballot)));
+            base = __shfl(base, leader);
+            if (take)
+            {
+                const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo(
+                                                                          static_cast<uint32_t>(ballot), 0u));
+                if (pos < static_cast<uint32_t>(kCandMax))
+                {
+                    sh.list_bits[pos] = b;
+                    sh.list_index[pos] = index;
+                }
+            }
+        }
+
+        // The list entries at or above its k-th largest (k <= nl <= kCandMax)
+        // go to the row's candidates, counted in sh.found.
+        __device__ __forceinline__ void emit_list(SelShared &sh, uint32_t nl, uint32_t k, int64_t row,
+                                                  const CandOut &co)
+        {
+            const uint32_t kth = block_kth([&](int i) { return sel_key(sh.list_bits[i]); }, static_cast<int>(nl), k,
+                                           sh.hist, sh.sel);
+            for (int i = threadIdx.x; i < static_cast<int>(nl); i += kSelBlock)
+            {
+                const uint32_t b = sh.list_bits[i];
+                if (sel_key(b) >= kth)
+                {
+                    const uint32_t slot = atomicAdd(&sh.found, 1u);
+                    if (slot < static_cast<uint32_t>(co.cap))
+                    {
+                        co.cand_index[row * co.cap + slot] = sh.list_index[i];
+                        co.cand_logit[row * co.cap + slot] = static_cast<uint16_t>(b);
+                    }
+                }
+            }
+        }
+
+        // Radix select over the whole row (per-wave histograms), then every
+        // logit at or above the k-th largest goes to the candidates.
+        __device__ void whole_row_select(const uint16_t *r, int64_t n, uint32_t k, int64_t row, const CandOut &co,
+                                         SelShared &sh)
+        {
+            const int tid = threadIdx.x;
+            uint32_t *my_hist = sh.wave_hist[tid / kWave];
+            auto clear = [&]() __attribute__((always_inline)) {
+                for (int i = tid; i < kSelWaves * 256; i += kSelBlock)
+                    (&sh.wave_hist[0][0])[i] = 0u;
+            };
+            auto merge = [&]() __attribute__((always_inline)) {
+                if (tid < 256)
+                {
+                    uint32_t sum = 0u;
+#pragma unroll
+                    for (int w = 0; w < kSelWaves; ++w)
+                        sum += sh.wave_hist[w][tid];
+                    sh.hist[tid] = sum;
+                }
+            };
+            clear();
+            __syncthreads();
+            for_row(r, 0, n, [&](int64_t, uint32_t b) __attribute__((always_inline)) {
+                atomicAdd(&my_hist[sel_key(b) >> 8], 1u);
+            });
+            __syncthreads();
+            merge();
+            __syncthreads();
+            if (tid < kWave)
+                find_bin(sh.hist, k, &sh.sel[0], &sh.sel[1]);
+            clear();
+            __syncthreads();
+            const uint32_t hi = sh.sel[0], rank = sh.sel[1];
+            for_row(r, 0, n, [&](int64_t, uint32_t b) __attribute__((always_inline)) {
+                const uint32_t key = sel_key(b);
+                if ((key >> 8) == hi)
+                    atomicAdd(&my_hist[key & 255u], 1u);
+            });
+            __syncthreads();
+            merge();
+            __syncthreads();
+            if (tid < kWave)
+            {
+                uint32_t unused;
+                find_bin(sh.hist, rank, &sh.sel[2], &unused);
+            }
+            __syncthreads();
+            if (tid == 0)
+                sh.sel[2] = (hi << 8) | sh.sel[2];
+            __syncthreads();
+            const uint32_t kth = sh.sel[2];
+            for_row(r, 0, n, [&](int64_t c, uint32_t b) __attribute__((always_inline)) {
+                if (sel_key(b) >= kth)
+                {
+                    const uint32_t slot = atomicAdd(&sh.found, 1u);
+                    if (slot < static_cast<uint32_t>(co.cap))
+                    {
+                        co.cand_index[row * co.cap + slot] = static_cast<int32_t>(c);
+                        co.cand_logit[row * co.cap + slot] = static_cast<uint16_t>(b);
+                    }
+                }
+            });
+        }
+
+        // The lower bound of the logits of [begin, end): the k-th largest of
+        // the thread maxima as a value (-inf when fewer than k threads hold
+        // logits: every logit is then taken), and its key in *key.
+        __device__ __forceinline__ float maxima_bound(SelShared &sh, uint32_t k, uint32_t *key)
+        {
+            const uint32_t t_key = block_kth([&](int i) { return sh.thread_max[i]; }, kSelBlock, k, sh.hist, sh.sel);
+            *key = t_key;
+            return t_key == 0u ? -__builtin_huge_valf() : bf_val(key_bits(t_key));
+        }
+
         __global__ __launch_bounds__(kSelBlock) void topk_select_kernel(const uint16_t *__restrict__ x, int64_t rows,
                                                                         int64_t stride, int64_t n, uint32_t k,
-                                                                        int32_t cap, int32_t *__restrict__ count,
-                                                                        int32_t *__restrict__ cand_index,
-                                                                        uint16_t *__restrict__ cand_logit,
+                                                                        CandOut co, int32_t *__restrict__ count,
                                                                         int32_t *__restrict__ nonfinite)
         {
-            __shared__ uint32_t wave_hist[kSelWaves][256];
-            __shared__ uint32_t hist[256];
-            __shared__ uint32_t thread_max[kSelBlock];
-            __shared__ uint32_t list_bits[kCandMax];
-            __shared__ int32_t list_index[kCandMax];
-            __shared__ uint32_t sel[3];
-            __shared__ uint32_t found, bad, listed;
+            __shared__ SelShared sh;
             const int tid = threadIdx.x;
-            const int lane = tid % kWave;
-            const int wave = tid / kWave;
             for (int64_t row = blockIdx.x; row < rows; row += gridDim.x)
             {
                 const uint16_t *r = x + row * stride;
                 if (tid == 0)
                 {
-                    found = 0u;
-                    bad = 0u;
-                    listed = 0u;
+                    sh.found = 0u;
+                    sh.bad = 0u;
+                    sh.listed = 0u;
                 }
                 __syncthreads();
-                // 1. per-thread maximum and non-finite flag
-                float tmax = -__builtin_huge_valf();
-                uint32_t my_bad = 0u;
-                for_row(r, n, [&](int64_t, uint32_t b) {
-                    my_bad |= (b & 0x7f80u) == 0x7f80u ? 1u : 0u;
-                    tmax = fmaxf(tmax, bf_val(b));
-                });
-                // a thread without logits counts as key 0, below every finite key
-                thread_max[tid] = tmax == -__builtin_huge_valf() ? 0u : sel_key(__float_as_uint(tmax) >> 16);
-                if (my_bad)
-                    atomicOr(&bad, 1u);
-                __syncthreads();
+                // 1. per-thread maxima and the non-finite flag
+                thread_maxima(r, 0, n, sh);
                 bool exact = false;
-                uint32_t kth = 0u;
                 // rows with a non-finite logit keep the whole-row select
-                if (k <= static_cast<uint32_t>(kSelBlock) && bad == 0u)
+                if (k <= static_cast<uint32_t>(kSelBlock) && sh.bad == 0u)
                 {
-                    // 2. lower bound and the list of logits at or above it; fewer
-                    // than k threads holding logits gives key 0: take every logit
-                    const uint32_t t_key = block_kth([&](int i) { return thread_max[i]; }, kSelBlock, k, hist, sel);
-                    const float t_val = t_key == 0u ? -__builtin_huge_valf() : bf_val(key_bits(t_key));
-                    for_row(r, n, [&](int64_t c, uint32_t b) {
-                        const bool take = bf_val(b) >= t_val;
-                        const uint64_t ballot = __ballot(take);
-                        if (ballot == 0)
-                            return;
-                        const int leader = __ffsll(static_cast<unsigned long long>(ballot)) - 1;
-                        uint32_t base = 0u;
-                        if (lane == leader)
-                            base = atomicAdd(&listed, static_cast<uint32_t>(__popcll(ballot)));
-                        base = __shfl(base, leader);
-                        if (take)
-                        {
-                            const uint32_t pos =
-                                base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo(
-                                                                     static_cast<uint32_t>(ballot), 0u));
-                            if (pos < static_cast<uint32_t>(kCandMax))
-                            {
-                                list_bits[pos] = b;
-                                list_index[pos] = static_cast<int32_t>(c);
-                            }
-                        }
+                    // 2. lower bound and the list of logits at or above it
+                    uint32_t t_key;
+                    const float t_val = maxima_bound(sh, k, &t_key);
+                    for_row(r, 0, n, [&](int64_t c, uint32_t b) __attribute__((always_inline)) {
+                        list_append(sh, bf_val(b) >= t_val, b, static_cast<int32_t>(c));
                     });
                     __syncthreads();
-                    const uint32_t nl = listed;
+                    const uint32_t nl = sh.listed;
                     if (nl <= static_cast<uint32_t>(kCandMax))
                     {
                         // 3. exact k-th over the list (k <= nl: the bound holds)
-                        kth = block_kth([&](int i) { return sel_key(list_bits[i]); }, static_cast<int>(nl), k, hist,
-                                        sel);
-                        for (int i = tid; i < static_cast<int>(nl); i += kSelBlock)
-                        {
-                            const uint32_t b = list_bits[i];
-                            if (sel_key(b) >= kth)
-                            {
-                                const uint32_t slot = atomicAdd(&found, 1u);
-                                if (slot < static_cast<uint32_t>(cap))
-                                {
-                                    cand_index[row * cap + slot] = list_index[i];
-                                    cand_logit[row * cap + slot] = static_cast<uint16_t>(b);
-                                }
-                            }
-                        }
+                        emit_list(sh, nl, k, row, co);
                         exact = true;
                     }
                 }
                 if (!exact)
-                {
-                    // radix select over the whole row: per-wave histograms
-                    uint32_t *my_hist = wave_hist[wave];
-                    auto clear = [&]() {
-                        for (int i = tid; i < kSelWaves * 256; i += kSelBlock)
-                            (&wave_hist[0][0])[i] = 0u;
-                    };
-                    auto merge = [&]() {
-                        if (tid < 256)
-                        {
-                            uint32_t sum = 0u;
-#pragma unroll
-                            for (int w = 0; w < kSelWaves; ++w)
-                                sum += wave_hist[w][tid];
-                            hist[tid] = sum;
-                        }
-                    };
-                    clear();
-                    __syncthreads();
-                    for_row(r, n, [&](int64_t, uint32_t b) { atomicAdd(&my_hist[sel_key(b) >> 8], 1u); });
-                    __syncthreads();
-                    merge();
-                    __syncthreads();
-                    if (tid == 0)
-                        find_bin(hist, k, &sel[0], &sel[1]);
-                    clear();
-                    __syncthreads();
-                    const uint32_t hi = sel[0], rank = sel[1];
-                    for_row(r, n, [&](int64_t, uint32_t b) {
-                        const uint32_t key = sel_key(b);
-                        if ((key >> 8) == hi)
-                            atomicAdd(&my_hist[key & 255u], 1u);
-                    });
-                    __syncthreads();
-                    merge();
-                    __syncthreads();
-                    if (tid == 0)
-                    {
-                        uint32_t lo, unused;
-                        find_bin(hist, rank, &lo, &unused);
-                        sel[2] = (hi << 8) | lo;
-                    }
-                    __syncthreads();
-                    kth = sel[2];
-                    for_row(r, n, [&](int64_t c, uint32_t b) {
-                        if (sel_key(b) >= kth)
-                        {
-                            const uint32_t slot = atomicAdd(&found, 1u);
-                            if (slot < static_cast<uint32_t>(cap))
-                            {
-                                cand_index[row * cap + slot] = static_cast<int32_t>(c);
-                                cand_logit[row * cap + slot] = static_cast<uint16_t>(b);
-                            }
-                        }
-                    });
-                }
+                    whole_row_select(r, n, k, row, co, sh);
                 __syncthreads();
                 if (tid == 0)
                 {
-                    count[row] = static_cast<int32_t>(found);
-                    nonfinite[row] = static_cast<int32_t>(bad);
+                    count[row] = static_cast<int32_t>(sh.found);
+                    nonfinite[row] = static_cast<int32_t>(sh.bad);
                 }
                 __syncthreads(); // the shared counters are reset for the next row
             }
+        }
+
+        // Sliced rows (few rows, k <= kSelBlock).  Per (row, slice): the
+        // slice's bound T_s (k-th largest of its thread maxima) and its logits
+        // at or above T_s.  The k threads whose maxima reach T_s hold k logits
+        // >= T_s, so the row's k-th largest is >= T_s, and >= T = max_s T_s;
+        // every top-k logit is >= the T_s of its own slice, so it is in that
+        // slice's list.  The merge keeps the listed logits >= T and selects
+        // exactly over them.
+        constexpr int kSliceCand = 2048;
+
+        struct SliceWork
+        {
+            uint32_t *header; // [rows * slices][4]: bound key, listed count, non-finite flag, 0
+            uint32_t *bits;   // [rows * slices][kSliceCand]
+            int32_t *index;   // [rows * slices][kSliceCand]
+            int32_t slices;
+            int64_t slice_len;
+        };
+
+        __global__ __launch_bounds__(kSelBlock) void topk_slice_kernel(const uint16_t *__restrict__ x, int64_t stride,
+                                                                       int64_t n, uint32_t k, SliceWork w)
+        {
+            __shared__ SelShared sh;
+            const int tid = threadIdx.x;
+            const int64_t slot = blockIdx.x;
+            const int64_t row = slot / w.slices;
+            const int64_t begin = (slot % w.slices) * w.slice_len;
+            const int64_t end = begin + w.slice_len < n ? begin + w.slice_len : n;
+            const uint16_t *r = x + row * stride;
+            if (tid == 0)
+            {
+                sh.bad = 0u;
+                sh.listed = 0u;
+            }
+            __syncthreads();
+            thread_maxima(r, begin, end, sh);
+            uint32_t t_key = 0u;
+            if (sh.bad == 0u)
+            {
+                const float t_val = maxima_bound(sh, k, &t_key);
+                for_row(r, begin, end, [&](int64_t c, uint32_t b) __attribute__((always_inline)) {
+                    list_append(sh, bf_val(b) >= t_val, b, static_cast<int32_t>(c));
+                });
+                __syncthreads();
+                const uint32_t nl = sh.listed;
+                const int kept = static_cast<int>(nl < static_cast<uint32_t>(kSliceCand) ? nl : kSliceCand);
+                for (int i = tid; i < kept; i += kSelBlock)
+                {
+                    w.bits[slot * kSliceCand + i] = sh.list_bits[i];
+                    w.index[slot * kSliceCand + i] = sh.list_index[i];
+                }
+            }
+            if (tid == 0)
+            {
+                w.header[4 * slot + 0] = t_key;
+                w.header[4 * slot + 1] = sh.listed;
+                w.header[4 * slot + 2] = sh.bad;
+                w.header[4 * slot + 3] = 0u;
+            }
+        }
+
+        __global__ __launch_bounds__(kSelBlock) void topk_merge_kernel(const uint16_t *__restrict__ x, int64_t stride,
+                                                                       int64_t n, uint32_t k, SliceWork w, CandOut co,
+                                                                       int32_t *__restrict__ count,
+                                                                       int32_t *__restrict__ nonfinite)
+        {
+            __shared__ SelShared sh;
+            const int tid = threadIdx.x;
+            const int64_t row = blockIdx.x;
+            const uint32_t *hdr = w.header + 4 * row * w.slices;
+            if (tid == 0)
+            {
+                sh.found = 0u;
+                sh.bad = 0u;
+                sh.listed = 0u;
+                sh.bound = 0u;
+                sh.overflow = 0u;
+            }
+            __syncthreads();
+            if (tid < w.slices)
+            {
+                atomicMax(&sh.bound, hdr[4 * tid + 0]);
+                if (hdr[4 * tid + 1] > static_cast<uint32_t>(kSliceCand))
+                    atomicOr(&sh.overflow, 1u);
+                if (hdr[4 * tid + 2] != 0u)
+                    atomicOr(&sh.bad, 1u);
+            }
+            __syncthreads();
+            bool exact = false;
+            if (sh.bad == 0u && sh.overflow == 0u)
+            {
+                // each slice's list is read by its own group of threads, so
+                // the lists of all slices are in flight together
+                const uint32_t bound = sh.bound;
+                const int per = kSelBlock / w.slices;
+                const int sp = tid / per;
+                if (sp < w.slices)
+                {
+                    const int64_t slot = row * w.slices + sp;
+                    const int listed = static_cast<int>(hdr[4 * sp + 1]);
+                    for (int i = tid % per; i < listed; i += per)
+                    {
+                        const uint32_t b = w.bits[slot * kSliceCand + i];
+                        list_append(sh, sel_key(b) >= bound, b, w.index[slot * kSliceCand + i]);
+                    }
+                }
+                __syncthreads();
+                const uint32_t nl = sh.listed;
+                if (nl <= static_cast<uint32_t>(kCandMax))
+                {
+                    emit_list(sh, nl, k, row, co);
+                    exact = true;
+                }
+            }
+            if (!exact)
+                whole_row_select(x + row * stride, n, k, row, co, sh);
+            __syncthreads();
+            if (tid == 0)
+            {
+                count[row] = static_cast<int32_t>(sh.found);
+                nonfinite[row] = static_cast<int32_t>(sh.bad);
+            }
+        }
+
+        // Rows are cut into slices when fewer than kTargetBlocks blocks would
+        // run (and k <= kSelBlock); a slice keeps at least kMinSlice logits.
+        constexpr int64_t kTargetBlocks = 512;
+        constexpr int64_t kMinSlice = 8 * kSelBlock;
+        constexpr int kMaxSlices = kWave;
+
+        struct SlicePlan
+        {
+            int32_t slices = 1;
+            int64_t slice_len = 0;
+            int64_t bytes = 0;
+        };
+
+        SlicePlan plan_slices(int64_t rows, int64_t n, int32_t k)
+        {
+            SlicePlan p;
+            if (rows <= 0 || rows >= kTargetBlocks || k <= 0 || k > kSelBlock)
+                return p;
+            int64_t want = (kTargetBlocks + rows - 1) / rows;
+            if (want > n / kMinSlice)
+                want = n / kMinSlice;
+            if (want > kMaxSlices)
+                want = kMaxSlices;
+            if (want < 2)
+                return p;
+            const int64_t len = ((n + want - 1) / want + 7) / 8 * 8;
+            const int64_t slices = (n + len - 1) / len;
+            if (slices < 2)
+                return p;
+            p.slices = static_cast<int32_t>(slices);
+            p.slice_len = len;
+            p.bytes = rows * slices * (4 * static_cast<int64_t>(sizeof(uint32_t)) + kSliceCand * 8);
+            return p;
         }
     } // namespace
 } // namespace q3k
@@ -312,7 +554,7 @@ namespace q3k
 extern "C" int q3k_topk_candidates_bf16(const uint16_t *logits, int64_t rows, int64_t row_stride,
                                         int64_t search_size, int32_t k, int32_t cap, int32_t *count,
                                         int32_t *cand_index, uint16_t *cand_logit, int32_t *nonfinite,
-                                        q3k_stream_t stream)
+                                        void *workspace, int64_t workspace_bytes, q3k_stream_t stream)
 {
     using namespace q3k;
     if (rows < 0)
@@ -325,6 +567,8 @@ extern "C" int q3k_topk_candidates_bf16(const uint16_t *logits, int64_t rows, in
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "top_k must be in [1, valid_vocab_size]");
     if (cap <= 0)
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "candidate capacity must be positive");
+    if (workspace_bytes < 0)
+        return set_error(Q3K_ERR_INVALID_ARGUMENT, "top-k workspace size cannot be negative");
     if (rows == 0)
         return Q3K_OK;
     if (logits == nullptr || count == nullptr || cand_index == nullptr || cand_logit == nullptr ||
@@ -335,9 +579,31 @@ extern "C" int q3k_topk_candidates_bf16(const uint16_t *logits, int64_t rows, in
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "top-k pointers must be aligned to their element size");
     if (rows > INT64_MAX / row_stride || rows > INT64_MAX / cap)
         return set_error(Q3K_ERR_OVERFLOW, "top-k sizes overflow");
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const CandOut co{cap, cand_index, cand_logit};
+    const SlicePlan plan = plan_slices(rows, search_size, k);
+    if (plan.slices > 1 && workspace != nullptr && workspace_bytes >= plan.bytes && aligned_to(workspace, 16))
+    {
+        const int64_t slots = rows * plan.slices;
+        SliceWork w;
+        w.header = static_cast<uint32_t *>(workspace);
+        w.bits = w.header + 4 * slots;
+        w.index = reinterpret_cast<int32_t *>(w.bits + slots * kSliceCand);
+        w.slices = plan.slices;
+        w.slice_len = plan.slice_len;
+        topk_slice_kernel<<<dim3(static_cast<unsigned>(slots)), dim3(kSelBlock), 0, s>>>(
+            logits, row_stride, search_size, static_cast<uint32_t>(k), w);
+        topk_merge_kernel<<<dim3(static_cast<unsigned>(rows)), dim3(kSelBlock), 0, s>>>(
+            logits, row_stride, search_size, static_cast<uint32_t>(k), w, co, count, nonfinite);
+        return check_launch("topk_candidates");
+    }
     const unsigned grid = static_cast<unsigned>(rows < 65535 ? rows : 65535);
-    topk_select_kernel<<<dim3(grid), dim3(kSelBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        logits, rows, row_stride, search_size, static_cast<uint32_t>(k), cap, count, cand_index, cand_logit,
-        nonfinite);
+    topk_select_kernel<<<dim3(grid), dim3(kSelBlock), 0, s>>>(logits, rows, row_stride, search_size,
+                                                               static_cast<uint32_t>(k), co, count, nonfinite);
     return check_launch("topk_candidates");
+}
+
+extern "C" int64_t q3k_topk_workspace_bytes(int64_t rows, int64_t search_size, int32_t k)
+{
+    return q3k::plan_slices(rows, search_size, k).bytes;
 }

@@ -32,9 +32,12 @@ namespace qwen3::ops
         Tensor output = Tensor::empty(Shape(std::move(dims)), DType::Int32, input.device());
         if (rows == 0)
             return output;
+        // few rows are cut into slices searched by separate blocks; the slice results need a workspace
+        const std::int64_t ws_bytes = q3k_argmax_workspace_bytes(rows, search);
+        Tensor workspace = Tensor::empty(Shape{(ws_bytes + 3) / 4}, DType::Int32, input.device());
         detail::launch_on(input.device(), [&](q3k_stream_t stream) {
             return q3k_argmax_bf16(detail::bf16_ptr(input), static_cast<int32_t *>(output.data()), rows, row_stride,
-                                   search, stream);
+                                   search, ws_bytes > 0 ? workspace.data() : nullptr, ws_bytes, stream);
         });
         return output;
     }

@@ -165,4 +165,28 @@ def test_argmax_argument_errors(q3k):
     msg = _expect(q3k.argmax, ValueError, IA, fake, fake, 2, 100, 101)
     assert "valid reduction size" in msg
     _expect(q3k.argmax, ValueError, IA, None, fake, 2, 100, 100)
+    msg = _expect(q3k.argmax, ValueError, IA, fake, fake, 2, 100, 100, None, fake, -8)
+    assert "workspace" in msg
     q3k.argmax(None, None, 0, 100, 100)
+
+
+def test_selection_workspace_plans(q3k):
+    """Argmax and top-k ask for a workspace only when the rows are too few to fill the GPU (and, for top-k, k fits
+    the bound step); the size covers one 8-byte key per slice, or a header and a list per slice."""
+    V = 151936
+    ws = q3k.argmax_workspace_bytes(64, V)
+    assert ws > 0 and ws % (64 * 8) == 0 and 2 <= ws // (64 * 8) <= 64
+    assert q3k.argmax_workspace_bytes(1, V) > 0
+    assert q3k.argmax_workspace_bytes(512, V) == 0        # enough rows: one block per row
+    assert q3k.argmax_workspace_bytes(4, 10000) == 0      # a row too short to cut
+    assert q3k.argmax_workspace_bytes(0, V) == 0
+    tk = q3k.topk_workspace_bytes(64, V, 20)
+    assert tk > 0 and tk % 64 == 0
+    assert q3k.topk_workspace_bytes(64, V, 1024) == tk    # the size does not depend on k up to the thread count
+    assert q3k.topk_workspace_bytes(64, V, 1025) == 0     # k above the thread count: whole-row select
+    assert q3k.topk_workspace_bytes(600, V, 20) == 0
+    IA = q3k.Q3K_ERR_INVALID_ARGUMENT
+    fake = 256
+    msg = _expect(q3k.topk_candidates, ValueError, IA, fake, 2, 100, 100, 5, 8, fake, fake, fake, fake, None, fake,
+                  -1)
+    assert "workspace" in msg

@@ -624,13 +624,18 @@ def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, n
 
 # ---------------------------------------------------------------- argmax
 
+@pytest.mark.parametrize("split", [False, True], ids=["whole", "sliced"])
 @pytest.mark.parametrize("rows,N,search,offset", [(2, 513, 0, 0), (37, 1000, 0, 0), (64, 151936, 0, 0),
                                                   (1, 151936, 151669, 0), (5, 1003, 0, 2), (3, 4096, 77, 2),
-                                                  (700, 64, 0, 0)])
-def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset):
-    """argmax_last_dimension (argmax.cu:34-100): bit-exact indices, including NaN rows, ties, +-0, +-inf and a
-    valid-vocabulary prefix of padded logits."""
-    name = f"argmax rows={rows} N={N} search={search} offset={offset}"
+                                                  (700, 64, 0, 0), (9, 40000, 0, 0), (2, 70001, 0, 2)])
+def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset, split):
+    """argmax_last_dimension (argmax.cu:34-100): bit-exact indices, including NaN rows, ties (also across slices),
+    +-0, +-inf and a valid-vocabulary prefix of padded logits; with the workspace the library asks for, few rows
+    are cut into slices searched by separate blocks, with the same result."""
+    ws_bytes = q3k.argmax_workspace_bytes(rows, search or N) if split else 0
+    if split and ws_bytes == 0:
+        pytest.skip("rows not sliced at this shape")
+    name = f"argmax rows={rows} N={N} search={search} offset={offset} split={split}"
     announce(name)
     if (rows, N) == (2, 513):
         x, _ = kat.argmax_inputs()
@@ -644,27 +649,36 @@ def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset):
             x[4, 5] = x[4, N - 2] = 0x7f80
             x[5, :] = 0x7fc0
             x[6, 9] = x[6, 3] = synth.f32_to_bf16(np.array([50.0], np.float32))[0]
+        if rows > 7:
+            x[7, N // 2] = x[7, N - 1] = synth.f32_to_bf16(np.array([60.0], np.float32))[0]
     X = Guarded(hip, x, offset=offset)
     O = Guarded(hip, nbytes=rows * 4)
-    q3k.argmax(X, O, rows, N, search or N)
+    W = Guarded(hip, nbytes=ws_bytes) if ws_bytes else None
+    q3k.argmax(X, O, rows, N, search or N, workspace=W, workspace_bytes=ws_bytes)
     hip.synchronize()
-    assert X.guards_intact() and O.guards_intact()
+    assert X.guards_intact() and O.guards_intact() and (W is None or W.guards_intact())
     check_exact(name, O.get(np.int32, (rows,)).view(np.uint32), oracle.argmax(x, search).view(np.uint32))
 
 
 # ---------------------------------------------------------------- sampling: top-k candidates
 
+@pytest.mark.parametrize("split", [False, True], ids=["whole", "sliced"])
 @pytest.mark.parametrize("rows,N,valid,k", [(8, 151936, 0, 20), (4, 151936, 151669, 1), (2, 151936, 0, 1024),
                                            (3, 5000, 0, 64), (2, 513, 500, 3),
                                            (2, 600, 0, 100),      # fewer than k threads hold logits: all listed
-                                           (2, 20000, 0, 1500)])  # k above the thread count: whole-row select
-def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k):
+                                           (2, 20000, 0, 1500),   # k above the thread count: whole-row select
+                                           (1, 151936, 151669, 50), (6, 40000, 0, 700)])
+def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k, split):
     """GPU top-k selection (the reference sampler's top-k rule, sampler.cpp:160-190): the candidate set equals the
-    oracle's exactly, ties at the k-th included; non-finite rows flagged."""
-    name = f"topk_candidates rows={rows} N={N} valid={valid} k={k}"
+    oracle's exactly, ties at the k-th included; non-finite rows flagged.  With the workspace the library asks for,
+    few rows are cut into slices (tied and non-finite rows then take the whole-row select), same set."""
+    n = valid or N
+    ws_bytes = q3k.topk_workspace_bytes(rows, n, k) if split else 0
+    if split and ws_bytes == 0:
+        pytest.skip("rows not sliced at this shape")
+    name = f"topk_candidates rows={rows} N={N} valid={valid} k={k} split={split}"
     announce(name)
     cap = 1024
-    n = valid or N
     x = synth.normal_bf16(174, N, (rows, N), std=3.0)
     x[0, 5] = x[0, 9] = x[0, 200] = x[0, 3]                     # ties
     x[0, 3] = synth.f32_to_bf16(np.array([40.0], np.float32))[0]
@@ -675,12 +689,18 @@ def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k):
     if rows > 3:
         x[3, n - 1] = 0x7f80                                     # non-finite inside the valid prefix
         x[3, N - 1] = 0x7fc0 if n < N else x[3, N - 1]
+    if rows > 4:
+        x[4, :] = synth.f32_to_bf16(np.array([-2.0], np.float32))[0]
+        x[4, n - 3 * k:n] = synth.normal_bf16(175, N, (3 * k,), std=1.0)   # the top k all in the last slice
+    if rows > 5:
+        x[5, ::997] = synth.f32_to_bf16(np.array([9.0], np.float32))[0]   # ties at the k-th spread over slices
     X = Guarded(hip, x)
     C, F = Guarded(hip, nbytes=rows * 4), Guarded(hip, nbytes=rows * 4)
     I, V = Guarded(hip, nbytes=rows * cap * 4), Guarded(hip, nbytes=rows * cap * 2)
-    q3k.topk_candidates(X, rows, N, n, k, cap, C, I, V, F)
+    W = Guarded(hip, nbytes=ws_bytes) if ws_bytes else None
+    q3k.topk_candidates(X, rows, N, n, k, cap, C, I, V, F, workspace=W, workspace_bytes=ws_bytes)
     hip.synchronize()
-    assert all(b.guards_intact() for b in (X, C, F, I, V))
+    assert all(b.guards_intact() for b in (X, C, F, I, V) + ((W,) if W is not None else ()))
     counts, flags = C.get(np.int32, (rows,)), F.get(np.int32, (rows,))
     ids, vals = I.get(np.int32, (rows, cap)), V.get(np.uint16, (rows, cap))
     for r in range(rows):
