@@ -2,8 +2,9 @@
 // in-place residual add.
 //
 // Fast path (16-byte aligned pointers): each thread streams UNROLL 128-bit
-// vectors (8 bf16) per operand, all loads issued before any arithmetic; a
-// wave's load instruction covers 1 KiB of contiguous memory.  The n % 8 tail
+// vectors (8 bf16) per operand (one for both ops, chosen by measurement),
+// all loads issued before any arithmetic; a wave's load instruction covers
+// 1 KiB of contiguous memory.  The n % 8 tail
 // is finished by a scalar pass in the first block.  Unaligned pointers take a
 // scalar grid-stride kernel.
 //
@@ -17,7 +18,7 @@ namespace q3k
     {
         // Launch shapes chosen by measurement on MI355X at the model's sizes:
         // vectors per thread (per operand) and non-temporal mode bits.
-        constexpr int kUnrollSilu = 2;
+        constexpr int kUnrollSilu = 1;  // config 4, sustained: 79-80% of peak against 77% for 2 and 74% for 4
         constexpr int kNtmSilu = 3;
         constexpr int kPrioSilu = 1;  // wave priority while loads are issued
         // XCD-contiguous tile remapping measured slower for both streams.
@@ -26,8 +27,6 @@ namespace q3k
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
         constexpr int kNtmCopy = 3;
-        // Below this many blocks at the unrolled shape a launch leaves CUs idle.
-        constexpr int64_t kSmallLaunchBlocks = 1024;
 
         // exp(x) for the SiLU denominator: Cody-Waite style split of
         // x * log2(e) into an integer and a fraction, the fraction through the
@@ -68,7 +67,12 @@ namespace q3k
                 den[j] = 1.0f + exp_f32(-gv[j]);
             const float m = fmaxf(fmaxf(fmaxf(den[0], den[1]), fmaxf(den[2], den[3])),
                                   fmaxf(fmaxf(den[4], den[5]), fmaxf(den[6], den[7])));
-            if (m < 0x1p126f || m != m)
+            const bool fast = m < 0x1p126f || m != m;
+            // The test is per lane, but its outcome is tested for the whole
+            // wave first: a lane-divergent if/else is issued on both sides
+            // under exec masks, and the IEEE divide would then cost every
+            // element ~12 more VALU ops.
+            if (__all(fast))
             {
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
@@ -78,7 +82,7 @@ namespace q3k
             {
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    s[j] = gv[j] / den[j];
+                    s[j] = fast ? gv[j] * __builtin_amdgcn_rcpf(den[j]) : gv[j] / den[j];
             }
         }
 
@@ -196,19 +200,8 @@ namespace q3k
             const int64_t blocks = (nvec + kVecPerBlock - 1) / kVecPerBlock;
             if (aligned16(a) && aligned16(b) && aligned16(out) && blocks < (int64_t{1} << 31))
             {
-                if (U > 1 && blocks < kSmallLaunchBlocks)
-                {
-                    // Few tokens (decode): one vector per thread puts U times
-                    // as many blocks on the CUs and halves each wave's chain.
-                    const int64_t b1 = (nvec + kBlock - 1) / kBlock;
-                    binary_vec_kernel<OP, 1, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(b1 > 0 ? b1 : 1)), dim3(kBlock), 0, stream>>>(
-                        a, b, out, nvec, n);
-                }
-                else
-                {
-                    binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
-                        a, b, out, nvec, n);
-                }
+                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
+                    a, b, out, nvec, n);
             }
             else
             {
