@@ -144,6 +144,35 @@ def time_chain(hip, stream, sets, make_ops, steps, warmup):
     return start.elapsed_ms(stop) / steps
 
 
+def time_chain_graph(hip, stream, sets, make_ops, steps, warmup):
+    """The chain over every input set captured into one HIP graph (one host
+    launch per cycle of the sets, as a serving loop replays a captured decode
+    step), replayed between one pair of events; returns ms per pass."""
+    per_set = [make_ops(s) for s in sets]
+
+    def record():
+        for ops in per_set:
+            for _, fn in ops:
+                fn()
+
+    graph = hip.Graph(stream, record)
+    try:
+        cycles = max(1, -(-steps // len(sets)))
+        for _ in range(max(1, -(-warmup // len(sets)))):
+            graph.launch(stream)
+        start, stop = hip.Event(), hip.Event()
+        hip.synchronize()
+        start.record(stream)
+        for _ in range(cycles):
+            graph.launch(stream)
+        stop.record(stream)
+        stop.synchronize()
+        hip.synchronize()
+        return start.elapsed_ms(stop) / (cycles * len(sets))
+    finally:
+        graph.destroy()
+
+
 # Buffers each chain op touches (for its own rotation when timed alone).
 OP_BUFFERS = {
     "add_rms_norm_attn": ("h1", "d1", "y1"),
@@ -393,6 +422,12 @@ def main():
                 "algorithmic_bytes": op_bytes[dominant]}
 
     extras = {}
+    # the same chain replayed from a HIP graph: no host launch cost between ops
+    # (what bounds the op-by-op loop at decode sizes)
+    ms_graph = time_chain_graph(hip, stream, sets, make_chain, args.steps, args.warmup)
+    extras["chain_graph_replay"] = {"ms_per_step": round(ms_graph, 5),
+                                    "GB/s": round(chain_bytes / (ms_graph * 1e-3) / 1e9, 1),
+                                    "pct_of_peak": round(100 * chain_bytes / (ms_graph * 1e-3) / 1e9 / PEAK_GBS, 2)}
     if not args.no_extras:
         print("[bench] timing unfused chain", file=sys.stderr, flush=True)
         make_unfused = lambda b: unfused_ops(q3k, c, b, stream)  # noqa: E731

@@ -16,6 +16,7 @@ from . import load as _load_q3k
 HIP_MEMCPY_H2D = 1
 HIP_MEMCPY_D2H = 2
 HIP_MEMCPY_D2D = 3
+HIP_STREAM_CAPTURE_MODE_THREAD_LOCAL = 1
 
 _hip = None
 
@@ -52,6 +53,12 @@ def runtime() -> ctypes.CDLL:
             "hipGetLastError": [],
             "hipDeviceGetAttribute": [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int],
             "hipMemGetInfo": [ctypes.POINTER(sz), ctypes.POINTER(sz)],
+            "hipStreamBeginCapture": [p, ctypes.c_int],
+            "hipStreamEndCapture": [p, ctypes.POINTER(p)],
+            "hipGraphInstantiate": [ctypes.POINTER(p), p, p, p, sz],
+            "hipGraphLaunch": [p, p],
+            "hipGraphExecDestroy": [p],
+            "hipGraphDestroy": [p],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -194,3 +201,45 @@ class Event:
         if self.ptr is not None:
             runtime().hipEventDestroy(self.ptr)
             self.ptr = None
+
+
+class Graph:
+    """The launches `record()` makes on `stream`, captured into a HIP graph
+    and instantiated for replay (hipStreamBeginCapture ... hipGraphInstantiate).
+    Nothing runs during capture; every replay runs the captured kernels with
+    the arguments they were launched with, so in-place ops act on whatever the
+    buffers hold at replay time."""
+
+    def __init__(self, stream: Stream, record):
+        rt = runtime()
+        check(rt.hipStreamBeginCapture(stream.ptr, HIP_STREAM_CAPTURE_MODE_THREAD_LOCAL), "hipStreamBeginCapture")
+        graph = ctypes.c_void_p()
+        try:
+            record()
+        except BaseException:
+            rt.hipStreamEndCapture(stream.ptr, ctypes.byref(graph))
+            if graph.value:
+                rt.hipGraphDestroy(graph.value)
+            raise
+        check(rt.hipStreamEndCapture(stream.ptr, ctypes.byref(graph)), "hipStreamEndCapture")
+        self.graph = graph.value
+        self.exec = None
+        exe = ctypes.c_void_p()
+        try:
+            check(rt.hipGraphInstantiate(ctypes.byref(exe), self.graph, None, None, 0), "hipGraphInstantiate")
+        except BaseException:
+            self.destroy()
+            raise
+        self.exec = exe.value
+
+    def launch(self, stream: Stream) -> None:
+        check(runtime().hipGraphLaunch(self.exec, stream.ptr), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        rt = runtime()
+        if self.exec is not None:
+            rt.hipGraphExecDestroy(self.exec)
+            self.exec = None
+        if self.graph is not None:
+            rt.hipGraphDestroy(self.graph)
+            self.graph = None
