@@ -20,8 +20,8 @@ D = 128
 
 def test_graph_replay_decode_step(q3k, hip, synth):
     """The c3 decode chain (add_rms_norm, qk_norm_rope with per-sequence positions, add_rms_norm, silu_mul), a
-    key-split decode attention and a sliced argmax, captured into one graph: three replays, each bit-identical to
-    the eager launches."""
+    key-split decode attention, a sliced argmax and a sliced top-k selection, captured into one graph: three
+    replays, each bit-identical to the eager launches."""
     announce("graph replay: decode step")
     B, H, I, Hq, Hkv, P = 64, 4096, 12288, 32, 8, 4096
     Bd, L, V = 4, 700, 20000   # attention over Bd sequences of L cached keys; argmax over [Bd, V]
@@ -41,12 +41,15 @@ def test_graph_replay_decode_step(q3k, hip, synth):
         "cache": q3k.build_rope_cache(P, D, 1e6),
     }
     bufs = {k: hip.DeviceBuffer.from_array(v) for k, v in arrays.items()}
-    outs = {"y1": B * H * 2, "y2": B * H * 2, "o": B * I * 2, "ao": Bd * Hq * D * 2, "ids": Bd * 4}
+    K, cap = 20, 256
+    outs = {"y1": B * H * 2, "y2": B * H * 2, "o": B * I * 2, "ao": Bd * Hq * D * 2, "ids": Bd * 4,
+            "cnt": Bd * 4, "bad": Bd * 4, "ci": Bd * cap * 4, "cv": Bd * cap * 2}
     bufs.update({k: hip.DeviceBuffer(n) for k, n in outs.items()})
     wa = q3k.gqa_attention_workspace_bytes(Bd, 1, Hq, Hkv, D, L)
     wm = q3k.argmax_workspace_bytes(Bd, V)
-    assert wa > 0 and wm > 0, "the decode shapes should take the split and sliced paths"
-    ws_a, ws_m = hip.DeviceBuffer(wa), hip.DeviceBuffer(wm)
+    wk = q3k.topk_workspace_bytes(Bd, V, K)
+    assert wa > 0 and wm > 0 and wk > 0, "the decode shapes should take the split and sliced paths"
+    ws_a, ws_m, ws_k = hip.DeviceBuffer(wa), hip.DeviceBuffer(wm), hip.DeviceBuffer(wk)
     st = (L * Hkv * D, Hkv * D, D, 1)
     stream = hip.Stream()
     b = bufs
@@ -59,6 +62,8 @@ def test_graph_replay_decode_step(q3k, hip, synth):
         q3k.gqa_attention(b["aq"], b["kc"], b["vc"], b["ao"], Bd, 1, Hq, Hkv, D, L, L - 1, st, st, stream,
                           workspace=ws_a, workspace_bytes=wa)
         q3k.argmax(b["logits"], b["ids"], Bd, V, V, stream, workspace=ws_m, workspace_bytes=wm)
+        q3k.topk_candidates(b["logits"], Bd, V, V, K, cap, b["cnt"], b["ci"], b["cv"], b["bad"], stream,
+                            workspace=ws_k, workspace_bytes=wk)
 
     changed = ("h1", "q", "k", "h2")   # rewritten in place by the step
 
@@ -69,8 +74,17 @@ def test_graph_replay_decode_step(q3k, hip, synth):
     def results():
         shapes = {"h1": ((B, H), np.uint16), "y1": ((B, H), np.uint16), "q": ((B, Hq * D), np.uint16),
                   "k": ((B, Hkv * D), np.uint16), "h2": ((B, H), np.uint16), "y2": ((B, H), np.uint16),
-                  "o": ((B, I), np.uint16), "ao": ((Bd, Hq * D), np.uint16), "ids": ((Bd,), np.int32)}
-        return {k: bufs[k].download(dt, sh) for k, (sh, dt) in shapes.items()}
+                  "o": ((B, I), np.uint16), "ao": ((Bd, Hq * D), np.uint16), "ids": ((Bd,), np.int32),
+                  "cnt": ((Bd,), np.int32), "bad": ((Bd,), np.int32)}
+        got = {k: bufs[k].download(dt, sh) for k, (sh, dt) in shapes.items()}
+        # candidates come in no particular order: compare each row's first count entries as sorted sets
+        ci = bufs["ci"].download(np.int32, (Bd, cap))
+        cv = bufs["cv"].download(np.uint16, (Bd, cap))
+        for r in range(Bd):
+            n = min(int(got["cnt"][r]), cap)
+            order = np.argsort(ci[r, :n], kind="stable")
+            got[f"cand{r}"] = np.concatenate([ci[r, :n][order].astype(np.int64), cv[r, :n][order].astype(np.int64)])
+        return got
 
     step()
     stream.synchronize()
