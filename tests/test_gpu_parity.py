@@ -716,6 +716,40 @@ def test_topk_candidates(q3k, hip, oracle, synth, rows, N, valid, k, split):
             check_exact(f"{name} row {r} logits", vals[r, :want.size], x[r, got])
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["whole", "sliced"])
+@pytest.mark.parametrize("rows,N,k,levels", [(1, 151936, 50, 16), (3, 50000, 7, 4), (17, 16385, 1, 64),
+                                             (2, 151936, 300, 2048), (5, 40001, 700, 32)])
+def test_topk_candidates_ties(q3k, hip, oracle, synth, rows, N, k, levels, split):
+    """Logits quantised to a few distinct values, so the k-th largest is tied many times over and the ties fall in
+    every slice: the candidate count and set equal the oracle's (a count above the capacity is reported as is)."""
+    n = N
+    ws_bytes = q3k.topk_workspace_bytes(rows, n, k) if split else 0
+    if split and ws_bytes == 0:
+        pytest.skip("rows not sliced at this shape")
+    name = f"topk ties rows={rows} N={N} k={k} levels={levels} split={split}"
+    announce(name)
+    cap = 1024
+    rng = np.random.default_rng(rows * 1000 + k)
+    vals = synth.f32_to_bf16(np.linspace(-4.0, 4.0, levels).astype(np.float32))
+    x = vals[rng.integers(0, levels, size=(rows, N))].astype(np.uint16)
+    X = Guarded(hip, x)
+    C, F = Guarded(hip, nbytes=rows * 4), Guarded(hip, nbytes=rows * 4)
+    I, V = Guarded(hip, nbytes=rows * cap * 4), Guarded(hip, nbytes=rows * cap * 2)
+    W = Guarded(hip, nbytes=ws_bytes) if ws_bytes else None
+    q3k.topk_candidates(X, rows, N, n, k, cap, C, I, V, F, workspace=W, workspace_bytes=ws_bytes)
+    hip.synchronize()
+    assert all(b.guards_intact() for b in (X, C, F, I, V) + ((W,) if W is not None else ()))
+    counts, flags = C.get(np.int32, (rows,)), F.get(np.int32, (rows,))
+    ids, cv = I.get(np.int32, (rows, cap)), V.get(np.uint16, (rows, cap))
+    for r in range(rows):
+        want = oracle.topk_set(x[r], k)
+        assert flags[r] == 0 and counts[r] == want.size, (r, counts[r], want.size)
+        if want.size <= cap:
+            got = ids[r, :want.size]
+            check_exact(f"{name} row {r} ids", np.sort(got), np.sort(want))
+            check_exact(f"{name} row {r} logits", cv[r, :want.size], x[r, got])
+
+
 @pytest.mark.parametrize("B,S,start,Hq,Hkv,cap", [(1, 1, 4095, 32, 8, 4096), (2, 5, 700, 32, 8, 800),
                                                  (1, 1, 300, 64, 8, 320), (1, 3, 400, 16, 8, 420),
                                                  (4, 1, 1000, 32, 8, 1100)])
