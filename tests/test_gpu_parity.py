@@ -660,6 +660,28 @@ def test_argmax(q3k, hip, oracle, synth, rows, N, search, offset, split):
     check_exact(name, O.get(np.int32, (rows,)).view(np.uint32), oracle.argmax(x, search).view(np.uint32))
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["whole", "sliced"])
+@pytest.mark.parametrize("rows,N,levels", [(1, 151936, 3), (7, 50000, 2), (33, 20000, 5), (2, 151936, 256)])
+def test_argmax_ties(q3k, hip, oracle, synth, rows, N, levels, split):
+    """Logits quantised to a few values, so the maximum is tied in many slices: the first index still wins."""
+    ws_bytes = q3k.argmax_workspace_bytes(rows, N) if split else 0
+    if split and ws_bytes == 0:
+        pytest.skip("rows not sliced at this shape")
+    name = f"argmax ties rows={rows} N={N} levels={levels} split={split}"
+    announce(name)
+    rng = np.random.default_rng(rows * 100 + levels)
+    vals = synth.f32_to_bf16(np.linspace(-3.0, 3.0, levels).astype(np.float32))
+    x = vals[rng.integers(0, levels, size=(rows, N))].astype(np.uint16)
+    x[0, : N // 2] = vals[0]   # row 0: the maximum appears only in the second half
+    X = Guarded(hip, x)
+    O = Guarded(hip, nbytes=rows * 4)
+    W = Guarded(hip, nbytes=ws_bytes) if ws_bytes else None
+    q3k.argmax(X, O, rows, N, N, workspace=W, workspace_bytes=ws_bytes)
+    hip.synchronize()
+    assert X.guards_intact() and O.guards_intact() and (W is None or W.guards_intact())
+    check_exact(name, O.get(np.int32, (rows,)).view(np.uint32), oracle.argmax(x).view(np.uint32))
+
+
 # ---------------------------------------------------------------- sampling: top-k candidates
 
 @pytest.mark.parametrize("split", [False, True], ids=["whole", "sliced"])
