@@ -8,6 +8,7 @@ Outputs (in-tree, git-ignored, shipped with the source tree to the GPU box):
                                ``qwen3::ops`` drop-in API, linked to libq3k.so.
 * ``tests/cpp/build/*``       C++ test executables (built only when their
                                sources exist).
+* ``bin/q3k_weight_io_bench``  the weight IO measurement (``bench/*.cpp``).
 * ``oracle/build/libq3k_oracle.so`` the CPU oracle (test infrastructure),
                                built through ``oracle/Makefile``.
 
@@ -31,6 +32,8 @@ KERNEL_DIR = os.path.join(PKG_DIR, "csrc", "kernels")
 HOST_DIRS = [os.path.join(PKG_DIR, "csrc", d) for d in ("core", "ops", "model", "generation", "io")]
 ORACLE_DIR = os.path.join(REPO_DIR, "oracle")
 CPP_TEST_DIR = os.path.join(REPO_DIR, "tests", "cpp")
+BENCH_DIR = os.path.join(PKG_DIR, "bench")
+BIN_DIR = os.path.join(PKG_DIR, "bin")
 
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -144,12 +147,28 @@ def build_cpp_tests(verbose=False) -> list[str]:
     return outs
 
 
+def build_benches(verbose=False) -> list[str]:
+    sources = sorted(glob.glob(os.path.join(BENCH_DIR, "*.cpp")))
+    os.makedirs(BIN_DIR, exist_ok=True)
+    jobs, outs = [], []
+    for src in sources:
+        exe = os.path.join(BIN_DIR, "q3k_" + os.path.splitext(os.path.basename(src))[0])
+        outs.append(exe)
+        jobs.append(["g++", *CXX_FLAGS, src, "-o", exe, f"-L{LIB_DIR}", "-lqwen3_runtime", "-lq3k",
+                     f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64",
+                     "-Wl,-rpath,$ORIGIN/" + os.path.relpath(LIB_DIR, BIN_DIR),
+                     f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}", "-pthread"])
+    _parallel(jobs, verbose)
+    return outs
+
+
 def build_all(verbose=False) -> dict:
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     result = {"kernels": build_kernels(verbose), "oracle": build_oracle(verbose)}
     result["runtime"] = build_runtime(verbose)
     result["cpp_tests"] = build_cpp_tests(verbose) if result["runtime"] else []
+    result["benches"] = build_benches(verbose) if result["runtime"] else []
     return result
 
 

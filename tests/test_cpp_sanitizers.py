@@ -1,5 +1,6 @@
 """The host-side C++ tests rebuilt with AddressSanitizer +
-UndefinedBehaviorSanitizer (g++, host code only; CPU only)."""
+UndefinedBehaviorSanitizer, and the loader's copy crew with ThreadSanitizer
+(g++, host code only; CPU only)."""
 import glob
 import os
 import shutil
@@ -23,10 +24,29 @@ def test_cpp_cpu_under_sanitizers():
             "-Wl,-rpath,/opt/rocm/lib", "-Wl,-rpath," + os.path.join(REPO, "oracle", "build"), "-pthread"]
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0", UBSAN_OPTIONS="print_stacktrace=1")
     with tempfile.TemporaryDirectory() as tmp:
-        for name in ["core_metadata_test", "tensor_view_test", "buffer_cpu_test", "tensor_cpu_test"]:
+        for name in ["core_metadata_test", "tensor_view_test", "buffer_cpu_test", "tensor_cpu_test", "copy_crew_cpu_test"]:
             exe = os.path.join(tmp, name)
             src = os.path.join(REPO, "tests", "cpp", name + ".cpp")
             build = subprocess.run(["g++", *flags, *inc, src, *core, "-o", exe, *libs], capture_output=True, text=True)
             assert build.returncode == 0, build.stderr[-3000:]
             proc = subprocess.run([exe], capture_output=True, text=True, timeout=120, env=env)
             assert proc.returncode == 0, f"{name} under sanitizers:\n{proc.stdout}\n{proc.stderr[-3000:]}"
+
+
+def test_copy_crew_under_thread_sanitizer():
+    """The staging copy crew (helper threads publishing and finishing copies through atomics) under -fsanitize=thread."""
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    inc = [f"-I{os.path.join(REPO, 'include')}", f"-I{os.path.join(REPO, 'oracle')}",
+           f"-I{os.path.join(REPO, 'tests', 'cpp')}"]
+    libs = [os.path.join(REPO, "oracle", "build", "libq3k_oracle.so"),
+            "-Wl,-rpath," + os.path.join(REPO, "oracle", "build"), "-pthread"]
+    with tempfile.TemporaryDirectory() as tmp:
+        exe = os.path.join(tmp, "copy_crew_tsan")
+        src = os.path.join(REPO, "tests", "cpp", "copy_crew_cpu_test.cpp")
+        build = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=thread", *inc, src, "-o", exe, *libs],
+                               capture_output=True, text=True)
+        assert build.returncode == 0, build.stderr[-3000:]
+        env = dict(os.environ, TSAN_OPTIONS="halt_on_error=1")
+        proc = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
+        assert proc.returncode == 0, f"copy crew under ThreadSanitizer:\n{proc.stdout}\n{proc.stderr[-3000:]}"
