@@ -1,5 +1,6 @@
-// The safetensors loader to the GPU: load() and the pinned double-buffered
-// load_many(), including a tensor larger than one 32 MiB staging buffer,
+// The safetensors loader to the GPU: load() and the pinned, staged
+// load_many() (a tensor larger than all staging buffers together, batches
+// large enough for the copy crew, an unknown name in such a batch),
 // byte-identical to the host load; the checkpoint's grouped load_many.
 #include "gpu_util.hpp"
 #include "qwen3/io/safetensors_checkpoint.h"
@@ -8,6 +9,8 @@
 #include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <stdexcept>
+#include <string>
 #include <unistd.h>
 
 namespace fs = std::filesystem;
@@ -39,7 +42,7 @@ namespace
         for (std::size_t i = 0; i < names.size(); ++i)
             require(on_gpu[i].device() == gpu && same_bytes(on_gpu[i], on_cpu[i]), "sharded tensors on the GPU");
 
-        // a 40 MiB bf16 tensor crosses both staging buffers
+        // a 40 MiB bf16 tensor wraps around the three 8 MiB staging buffers
         const fs::path d = fs::temp_directory_path() / ("q3k_io_gpu_" + std::to_string(::getpid()));
         fs::create_directories(d);
         const std::size_t n = 20u * 1024u * 1024u + 77u;
@@ -65,6 +68,15 @@ namespace
         require(same_bytes(many[0], big_host) && same_bytes(many[2], big_host), "40 MiB tensor through the staging");
         require(same_bytes(many[1], loader.load("small", cpu)), "small tensor after a large one");
         require(same_bytes(loader.load("big", gpu), big_host), "single load to the GPU");
+        // a batch large enough for the copy crew: an unknown name fails before any transfer
+        test::require_throws<std::out_of_range>([&] { (void)loader.load_many({"big", "missing", "big"}, gpu); },
+                                                "unknown name in a crew-sized batch");
+        // many chunks: the staging slots wrap several times, the small tensor between two large ones
+        const auto again = loader.load_many({"big", "big", "small", "big", "big"}, gpu);
+        require(again.size() == 5, "five results");
+        for (std::size_t i : {0u, 1u, 3u, 4u})
+            require(same_bytes(again[i], big_host), "repeated 40 MiB tensor " + std::to_string(i));
+        require(same_bytes(again[2], loader.load("small", cpu)), "small tensor among large ones");
         fs::remove_all(d);
         require(test::current_device() == before, "a load changed the current device");
     }
