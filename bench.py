@@ -369,6 +369,30 @@ def cpu_baseline(configs, synth, seconds):
     }
 
 
+def weight_io_extra(seconds_limit=180):
+    """The safetensors weight IO measurement (bin/q3k_weight_io_bench, a child process): a synthetic file of 4
+    Qwen3-8B layers (1.5 GB) in the page cache, loaded to the GPU by the loader and by the reference's staging
+    scheme, beside the host-to-device DMA ceiling."""
+    import subprocess
+    import tempfile
+
+    exe = os.path.join(REPO, "qwen3-runtime-byyourself_amd", "bin", "q3k_weight_io_bench")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} is not built"}
+    with tempfile.TemporaryDirectory() as d:
+        try:
+            proc = subprocess.run([exe, "--layers", "4", "--repeats", "3", "--dir", d], capture_output=True,
+                                  text=True, timeout=seconds_limit)
+        except subprocess.TimeoutExpired:
+            return {"error": f"timed out after {seconds_limit} s"}
+    if proc.returncode != 0 or not proc.stdout.strip():
+        return {"error": f"exit {proc.returncode}: {proc.stderr.strip()[-300:]}"}
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    return {"GB/s": r["loader"], "reference_scheme_GB/s": r["reference"], "dma_ceiling_GB/s": r["dma_ceiling"],
+            "bytes": r["bytes"], "vs_reference_scheme": round(r["loader"] / r["reference"], 2),
+            "frac_of_dma_ceiling": round(r["loader"] / r["dma_ceiling"], 3)}
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -541,6 +565,10 @@ def main():
             for e in emb_sets:
                 for buf in e.values():
                     buf.free()
+
+    if not args.no_extras:
+        print("[bench] weight IO", file=sys.stderr, flush=True)
+        extras["weight_io"] = weight_io_extra()
 
     cpu = None
     if not args.no_cpu_baseline:
