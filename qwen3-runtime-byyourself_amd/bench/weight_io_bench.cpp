@@ -140,12 +140,11 @@ namespace
     // slot_bytes is copied by `threads` host threads (the loader's copy crew)
     // into the next pinned slot (after that slot's previous DMA has
     // completed), then sent with an async copy on one stream.  threads = 1,
-    // slots = 2, 32 MiB with default pinned memory is the reference's scheme
-    // (cudaHostAllocDefault, src/io/safetensors_loader.cpp:92); the sweep
-    // uses the loader's coherent pinned memory.  Returns seconds from the
-    // mapping to the last DMA.
+    // slots = 2, 32 MiB is the reference's scheme (src/io/
+    // safetensors_loader.cpp:92 allocates with cudaHostAllocDefault, as this
+    // does).  Returns seconds from the mapping to the last DMA.
     double staged_load(const fs::path &path, const std::vector<std::string> &names, int threads, int slots,
-                       std::size_t slot_bytes, unsigned pin_flags, std::vector<qwen3::Tensor> &out)
+                       std::size_t slot_bytes, std::vector<qwen3::Tensor> &out)
     {
         const auto t0 = std::chrono::steady_clock::now();
         qwen3::SafetensorsFile file(path);
@@ -156,7 +155,7 @@ namespace
         std::vector<hipEvent_t> events(slots, nullptr);
         for (int i = 0; i < slots; ++i)
         {
-            QWEN3_HIP_CHECK(hipHostMalloc(&staging[i], slot_bytes, pin_flags));
+            QWEN3_HIP_CHECK(hipHostMalloc(&staging[i], slot_bytes, hipHostMallocDefault));
             QWEN3_HIP_CHECK(hipEventCreateWithFlags(&events[i], hipEventDisableTiming));
         }
         out.clear();
@@ -232,7 +231,7 @@ namespace
     {
         constexpr std::size_t ring = 64u << 20, slot = 32u << 20;
         void *host = nullptr;
-        QWEN3_HIP_CHECK(hipHostMalloc(&host, ring, hipHostMallocCoherent));
+        QWEN3_HIP_CHECK(hipHostMalloc(&host, ring, hipHostMallocDefault));
         const auto t0 = std::chrono::steady_clock::now();
         {
             qwen3::SafetensorsFile file(path);
@@ -276,7 +275,7 @@ namespace
         t0 = std::chrono::steady_clock::now();
         std::vector<void *> staging(qwen3::SafetensorsLoader::kStagingSlotCount, nullptr);
         for (auto &p : staging)
-            QWEN3_HIP_CHECK(hipHostMalloc(&p, qwen3::SafetensorsLoader::kStagingBufferBytes, hipHostMallocCoherent));
+            QWEN3_HIP_CHECK(hipHostMalloc(&p, qwen3::SafetensorsLoader::kStagingBufferBytes, hipHostMallocDefault));
         const double pin_s = seconds_since(t0);
         t0 = std::chrono::steady_clock::now();
         hipStream_t stream = nullptr;
@@ -360,7 +359,7 @@ int main(int argc, char **argv)
         std::vector<qwen3::Tensor> out;
         auto rate = [&](double s) { return gb / s; };
 
-        const double ref = best_of(repeats, [&] { return staged_load(path, names, 1, 2, 32u << 20, hipHostMallocDefault, out); });
+        const double ref = best_of(repeats, [&] { return staged_load(path, names, 1, 2, 32u << 20, out); });
         out.clear();
         std::fprintf(stderr, "[weight_io] reference scheme %.2f GB/s\n", rate(ref));
         const double ld = best_of(repeats, [&] { return loader_load(path, names, out); });
@@ -394,7 +393,7 @@ int main(int argc, char **argv)
                 for (int s : {2, 3, 4})
                     for (std::size_t mb : {4u, 8u, 16u, 32u})
                     {
-                        const double x = best_of(repeats, [&] { return staged_load(path, names, t, s, mb << 20, hipHostMallocCoherent, out); });
+                        const double x = best_of(repeats, [&] { return staged_load(path, names, t, s, mb << 20, out); });
                         out.clear();
                         std::fprintf(stderr, "[weight_io] sweep threads %d slots %d slot %zu MiB: %.2f GB/s\n", t, s,
                                      mb, rate(x));

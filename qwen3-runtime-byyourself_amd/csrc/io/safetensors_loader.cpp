@@ -72,10 +72,10 @@ namespace qwen3
             QWEN3_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
             for (std::size_t i = 0; i < kStagingSlotCount; ++i)
             {
-                // Coherent pinned memory comes back with its pages in place; the default kind
-                // faults on the first CPU write (~11 ms per 32 MiB, measured), which a single
-                // load would pay in full.
-                QWEN3_HIP_CHECK(hipHostMalloc(&staging_[i], kStagingBufferBytes, hipHostMallocCoherent));
+                // Fresh pinned memory faults on its first CPU write (the first memcpy into a new
+                // 32 MiB buffer measured 11 ms, the second 1.1 ms): small slots keep that cost,
+                // paid once per loader, low.
+                QWEN3_HIP_CHECK(hipHostMalloc(&staging_[i], kStagingBufferBytes, hipHostMallocDefault));
                 QWEN3_HIP_CHECK(hipEventCreateWithFlags(&events_[i], hipEventDisableTiming));
             }
         }
