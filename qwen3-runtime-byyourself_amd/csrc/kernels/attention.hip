@@ -503,11 +503,18 @@ namespace q3k
                 {
                     const int32_t key0 = tile * kKeyTile;
                     f32x16_t sacc[2];
+                    // The matrix phase (S = K Q^T, then the previous tile's P V)
+                    // runs at raised wave priority, the softmax at the default:
+                    // the other block's wave on the SIMD then interleaves its
+                    // VALU work instead of competing for issue with the MFMAs
+                    // (prefill 4% faster at config 4, decode unchanged).
+                    __builtin_amdgcn_s_setprio(1);
                     qk_tile(k_cur, qf, li, lg, sacc);
                     if (key0 + kKeyTile - 1 > start + wave_s0 || wave_partial)
                         mask_tile(sacc, key0, lg, last_key, col_ok);
                     if constexpr (decltype(with_pv)::value)
                         pv_tile(v_prev, v_off, phi, plo, o);
+                    __builtin_amdgcn_s_setprio(0);
                     const float alpha = softmax_tile(sacc, scale2, m, l, phi, plo);
                     // o holds the tiles before this one at the previous reference
                     rescale(o, alpha);
