@@ -111,11 +111,11 @@ def build_runtime(verbose=False) -> str | None:
         rel = os.path.relpath(src, os.path.join(PKG_DIR, "csrc")).replace(os.sep, "_")
         obj = os.path.join(obj_dir, rel + ".o")
         objects.append(obj)
-        jobs.append(["g++", *CXX_FLAGS, "-c", src, "-o", obj])
+        jobs.append(["g++", *CXX_FLAGS, "-pthread", "-c", src, "-o", obj])
     _parallel(jobs, verbose)
     out = os.path.join(LIB_DIR, "libqwen3_runtime.so")
     tmp = out + ".tmp"
-    _run(["g++", "-shared", "-o", tmp, *objects, f"-L{LIB_DIR}", "-lq3k",
+    _run(["g++", "-shared", "-pthread", "-o", tmp, *objects, f"-L{LIB_DIR}", "-lq3k",
           f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64", *RPATH], verbose=verbose)
     os.replace(tmp, out)
     return out
