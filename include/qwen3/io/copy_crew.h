@@ -1,8 +1,10 @@
 #pragma once
 
-// A crew of helper threads that splits one large memcpy with the calling
-// thread (used by SafetensorsLoader::load_many to fill its pinned staging
-// buffers from the mapped file).  Header-only so the host tests can build it
+// A crew of helper threads that splits one large host copy with the calling
+// thread (used by the safetensors upload to fill its pinned staging slots
+// from mapped files).  A copy is a list of segments; the crew treats them as
+// one concatenated byte range and cuts that range into equal parts of whole
+// 4 KiB pages, one per thread.  Header-only so the host tests can build it
 // under ThreadSanitizer.
 
 #include <algorithm>
@@ -17,9 +19,15 @@
 
 namespace qwen3::detail
 {
-    // copy() splits [0, bytes) into helpers + 1 parts of whole 4 KiB pages;
-    // the calling thread copies part 0 and each helper one other part, and
-    // copy() returns once every part is written.  copy() is called from one
+    // One piece of a gathered copy: `bytes` bytes from `src` to `dst`.
+    struct CopySegment
+    {
+        void *dst;
+        const void *src;
+        std::size_t bytes;
+    };
+
+    // copy() returns once every part is written, and is called from one
     // thread at a time.
     //
     // Hand-off: the caller stores the job, then bumps `sequence_` under the
@@ -53,17 +61,27 @@ namespace qwen3::detail
 
         void copy(void *dst, const void *src, std::size_t bytes)
         {
+            const CopySegment one{dst, src, bytes};
+            copy(&one, 1);
+        }
+
+        void copy(const CopySegment *segments, std::size_t count)
+        {
+            std::size_t total = 0;
+            for (std::size_t i = 0; i < count; ++i)
+                total += segments[i].bytes;
             const std::size_t parts = threads_.size() + 1;
-            if (parts == 1 || bytes == 0)
+            if (parts == 1 || total < kMinSplitBytes)
             {
-                if (bytes != 0)
-                    std::memcpy(dst, src, bytes);
+                for (std::size_t i = 0; i < count; ++i)
+                    if (segments[i].bytes != 0)
+                        std::memcpy(segments[i].dst, segments[i].src, segments[i].bytes);
                 return;
             }
-            dst_ = static_cast<std::byte *>(dst);
-            src_ = static_cast<const std::byte *>(src);
-            bytes_ = bytes;
-            part_ = ((bytes + parts - 1) / parts + 4095) & ~std::size_t{4095};
+            segments_ = segments;
+            count_ = count;
+            total_ = total;
+            part_ = ((total + parts - 1) / parts + 4095) & ~std::size_t{4095};
             remaining_.store(static_cast<int>(threads_.size()), std::memory_order_relaxed);
             {
                 std::lock_guard<std::mutex> lock(mutex_);
@@ -80,6 +98,8 @@ namespace qwen3::detail
 
     private:
         static constexpr int kPollRounds = 4096;
+        // below this many bytes the caller copies alone (waking the crew costs more)
+        static constexpr std::size_t kMinSplitBytes = 256 * 1024;
 
         static void pause() noexcept
         {
@@ -102,11 +122,25 @@ namespace qwen3::detail
             return ready();
         }
 
+        // Copies bytes [part * part_, (part + 1) * part_) of the concatenated segments.
         void copy_part(std::size_t part) const noexcept
         {
-            const std::size_t b = std::min(bytes_, part_ * part), e = std::min(bytes_, part_ * (part + 1));
-            if (b < e)
-                std::memcpy(dst_ + b, src_ + b, e - b);
+            std::size_t begin = std::min(total_, part_ * part);
+            const std::size_t end = std::min(total_, part_ * (part + 1));
+            std::size_t base = 0;  // offset of segment i in the concatenation
+            for (std::size_t i = 0; i < count_ && begin < end; ++i)
+            {
+                const CopySegment &s = segments_[i];
+                const std::size_t seg_end = base + s.bytes;
+                if (begin < seg_end)
+                {
+                    const std::size_t from = begin - base, to = std::min(end, seg_end) - base;
+                    std::memcpy(static_cast<std::byte *>(s.dst) + from, static_cast<const std::byte *>(s.src) + from,
+                                to - from);
+                    begin = base + to;
+                }
+                base = seg_end;
+            }
         }
 
         void run(std::size_t part)
@@ -153,9 +187,9 @@ namespace qwen3::detail
         std::atomic<std::uint64_t> sequence_{0};
         std::atomic<int> remaining_{0};
         std::atomic<bool> stop_{false};
-        std::byte *dst_ = nullptr;
-        const std::byte *src_ = nullptr;
-        std::size_t bytes_ = 0;
+        const CopySegment *segments_ = nullptr;
+        std::size_t count_ = 0;
+        std::size_t total_ = 0;
         std::size_t part_ = 0;
     };
 } // namespace qwen3::detail

@@ -32,6 +32,8 @@
 #include "qwen3/io/safetensors_loader.h"
 #include "qwen3/io/safetensors_metadata.h"
 
+#include "../csrc/io/staged_upload.hpp"
+
 #include <algorithm>
 #include <chrono>
 #include <cstdint>
@@ -273,9 +275,9 @@ namespace
         }
         const double alloc_s = seconds_since(t0);
         t0 = std::chrono::steady_clock::now();
-        std::vector<void *> staging(qwen3::SafetensorsLoader::kStagingSlotCount, nullptr);
+        std::vector<void *> staging(qwen3::io_detail::StagedUpload::kSlots, nullptr);
         for (auto &p : staging)
-            QWEN3_HIP_CHECK(hipHostMalloc(&p, qwen3::SafetensorsLoader::kStagingBufferBytes, hipHostMallocDefault));
+            QWEN3_HIP_CHECK(hipHostMalloc(&p, qwen3::io_detail::StagedUpload::kSlotBytes, hipHostMallocDefault));
         const double pin_s = seconds_since(t0);
         t0 = std::chrono::steady_clock::now();
         hipStream_t stream = nullptr;

@@ -1,180 +1,63 @@
-// Tensor loading from one safetensors file (behaviour of the reference's
-// src/io/safetensors_loader.cpp).  load(): one tensor, plain copy.
-// load_many() to a GPU: chunks of at most 8 MiB are copied from the mapped
-// file into the next of three pinned staging buffers and sent with an async
-// host-to-device copy on the loader's non-blocking stream; a buffer is
-// refilled once the event of its previous copy has completed, so the host
-// copies of the next chunks overlap the DMA of earlier ones.  Batches of at
-// least 32 MiB split each chunk's host copy over a crew of threads that
-// lives for the call: a single thread copies from a fresh mapping (page
-// faults included) at ~30 GB/s, about half of what the host-to-device link
-// carries.
+// SafetensorsLoader: one mapped file, its tensor table, and (for GPU
+// batches) a staged upload kept across calls.  The behaviour callers see is
+// that of the reference's src/io/safetensors_loader.cpp (results in request
+// order, unknown names rejected before any transfer, every byte on the
+// device when load_many returns); the transfer machinery is
+// io_detail::StagedUpload.
 #include "qwen3/io/safetensors_loader.h"
 
-#include "qwen3/hip/hip_check.h"
-#include "qwen3/io/copy_crew.h"
+#include "staged_upload.hpp"
 
-#include <algorithm>
-#include <cstring>
 #include <stdexcept>
-#include <thread>
 
 namespace qwen3
 {
-    namespace
-    {
-        unsigned copy_helpers(std::size_t total_bytes, unsigned max_threads)
-        {
-            if (total_bytes < SafetensorsLoader::kParallelCopyMinBytes)
-                return 0;
-            const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-            return std::min(max_threads, hw) - 1;
-        }
-    } // namespace
-
     SafetensorsLoader::SafetensorsLoader(const std::filesystem::path &model_path) : file_(model_path), metadata_(file_)
     {
     }
 
-    SafetensorsLoader::~SafetensorsLoader() { release_transfer_resources(); }
-
-    const std::byte *SafetensorsLoader::source_data(const SafetensorsTensorInfo &info) const noexcept
-    {
-        return file_.data_bytes().data() + info.begin_offset;
-    }
+    SafetensorsLoader::~SafetensorsLoader() = default;
 
     Tensor SafetensorsLoader::load(std::string_view tensor_name, Device target_device) const
     {
-        const SafetensorsTensorInfo &info = metadata_.tensor(tensor_name);
-        Tensor result = Tensor::empty(info.shape, info.dtype, target_device);
-        if (result.nbytes() != info.size_bytes())
-            throw std::logic_error("Tensor size does not match metadata for '" + std::string(tensor_name) + "'");
-        if (info.size_bytes() == 0)
-            return result;
-        if (target_device.is_cpu())
-        {
-            std::memcpy(result.data(), source_data(info), info.size_bytes());
-            return result;
-        }
-        hip::DeviceGuard guard(target_device.index());
-        QWEN3_HIP_CHECK(hipMemcpy(result.data(), source_data(info), info.size_bytes(), hipMemcpyHostToDevice));
-        return result;
-    }
-
-    void SafetensorsLoader::ensure_transfer_resources(int device_index)
-    {
-        if (stream_ != nullptr && transfer_device_ == device_index)
-            return;
-        release_transfer_resources();
-        transfer_device_ = device_index;
-        try
-        {
-            QWEN3_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
-            for (std::size_t i = 0; i < kStagingSlotCount; ++i)
-            {
-                // Fresh pinned memory faults on its first CPU write (the first memcpy into a new
-                // 32 MiB buffer measured 11 ms, the second 1.1 ms): small slots keep that cost,
-                // paid once per loader, low.
-                QWEN3_HIP_CHECK(hipHostMalloc(&staging_[i], kStagingBufferBytes, hipHostMallocDefault));
-                QWEN3_HIP_CHECK(hipEventCreateWithFlags(&events_[i], hipEventDisableTiming));
-            }
-        }
-        catch (...)
-        {
-            release_transfer_resources();
-            throw;
-        }
-    }
-
-    void SafetensorsLoader::release_transfer_resources() noexcept
-    {
-        if (transfer_device_ < 0)
-            return;
-        int previous = 0;
-        const bool restore = hipGetDevice(&previous) == hipSuccess;
-        (void)hipSetDevice(transfer_device_);
-        if (stream_ != nullptr)
-            (void)hipStreamSynchronize(stream_);
-        for (auto &e : events_)
-            if (e != nullptr)
-            {
-                (void)hipEventDestroy(e);
-                e = nullptr;
-            }
-        for (auto &b : staging_)
-            if (b != nullptr)
-            {
-                (void)hipHostFree(b);
-                b = nullptr;
-            }
-        if (stream_ != nullptr)
-        {
-            (void)hipStreamDestroy(stream_);
-            stream_ = nullptr;
-        }
-        transfer_device_ = -1;
-        if (restore)
-            (void)hipSetDevice(previous);
+        return io_detail::copy_out(file_, metadata_.tensor(tensor_name), target_device, tensor_name);
     }
 
     std::vector<Tensor> SafetensorsLoader::load_many(const std::vector<std::string> &tensor_names, Device target_device)
     {
-        std::vector<Tensor> results;
-        results.reserve(tensor_names.size());
+        std::vector<Tensor> out;
+        out.reserve(tensor_names.size());
         if (tensor_names.empty())
-            return results;
-        if (target_device.is_cpu())
-        {
-            for (const std::string &name : tensor_names)
-                results.push_back(load(name, target_device));
-            return results;
-        }
-        if (!target_device.is_cuda())
+            return out;
+        if (!target_device.is_cpu() && !target_device.is_cuda())
             throw std::invalid_argument("unsupported target device");
-        hip::DeviceGuard guard(target_device.index());
-        ensure_transfer_resources(target_device.index());
-        // every name is looked up before any transfer starts; each output is
-        // allocated just before its chunks, while earlier chunks are in flight
         std::vector<const SafetensorsTensorInfo *> infos;
         infos.reserve(tensor_names.size());
-        for (const std::string &name : tensor_names)
-            infos.push_back(&metadata_.tensor(name));
         std::size_t total = 0;
-        for (const SafetensorsTensorInfo *info : infos)
-            total += info->size_bytes();
-        std::array<bool, kStagingSlotCount> in_flight{};
-        std::size_t next = 0;
-        try
+        for (const std::string &name : tensor_names)
         {
-            detail::CopyCrew crew(copy_helpers(total, kCopyThreads));
-            for (std::size_t t = 0; t < infos.size(); ++t)
-            {
-                const SafetensorsTensorInfo &info = *infos[t];
-                results.push_back(Tensor::empty(info.shape, info.dtype, target_device));
-                if (results.back().nbytes() != info.size_bytes())
-                    throw std::logic_error("Tensor size does not match metadata for '" + tensor_names[t] + "'");
-                const std::byte *src = source_data(info);
-                auto *dst = static_cast<std::byte *>(results[t].data());
-                for (std::size_t done = 0; done < info.size_bytes();)
-                {
-                    const std::size_t slot = next++ % kStagingSlotCount;
-                    if (in_flight[slot])
-                        QWEN3_HIP_CHECK(hipEventSynchronize(events_[slot]));
-                    const std::size_t chunk = std::min(info.size_bytes() - done, kStagingBufferBytes);
-                    crew.copy(staging_[slot], src + done, chunk);
-                    QWEN3_HIP_CHECK(hipMemcpyAsync(dst + done, staging_[slot], chunk, hipMemcpyHostToDevice, stream_));
-                    QWEN3_HIP_CHECK(hipEventRecord(events_[slot], stream_));
-                    in_flight[slot] = true;
-                    done += chunk;
-                }
-            }
-            QWEN3_HIP_CHECK(hipStreamSynchronize(stream_));
+            infos.push_back(&metadata_.tensor(name));
+            total += infos.back()->size_bytes();
         }
-        catch (...)
+        if (target_device.is_cpu())
         {
-            (void)hipStreamSynchronize(stream_);
-            throw;
+            for (std::size_t i = 0; i < infos.size(); ++i)
+                out.push_back(io_detail::copy_out(file_, *infos[i], target_device, tensor_names[i]));
+            return out;
         }
-        return results;
+        if (!upload_ || upload_->device() != target_device.index())
+        {
+            upload_.reset();
+            upload_ = std::make_unique<io_detail::StagedUpload>(target_device.index());
+        }
+        const std::byte *data = file_.data_bytes().data();
+        upload_->run(infos.size(), total, [&](std::size_t i) {
+            const SafetensorsTensorInfo &info = *infos[i];
+            out.push_back(Tensor::empty(info.shape, info.dtype, target_device));
+            if (out.back().nbytes() != info.size_bytes())
+                throw std::logic_error("Tensor size does not match metadata for '" + tensor_names[i] + "'");
+            return io_detail::UploadPiece{data + info.begin_offset, out.back().data(), info.size_bytes()};
+        });
+        return out;
     }
 } // namespace qwen3

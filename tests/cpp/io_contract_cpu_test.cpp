@@ -1,0 +1,356 @@
+// The safetensors IO contract, one case per row: every check of the
+// reference's src/io/{safetensors_file,safetensors_metadata,
+// safetensors_checkpoint,mapped_file}.cpp with the exception type and the
+// message it raises (rows F*, M*, C*, L*), plus the pull parser's JSON
+// grammar (rows J*).  A case names its row in its failure message.
+#include "../../qwen3-runtime-byyourself_amd/csrc/io/json_cursor.hpp"
+#include "qwen3/io/mapped_file.h"
+#include "qwen3/io/safetensors_checkpoint.h"
+#include "qwen3/io/safetensors_file.h"
+#include "qwen3/io/safetensors_loader.h"
+#include "qwen3/io/safetensors_metadata.h"
+#include "test_util.hpp"
+
+#include <filesystem>
+#include <fstream>
+#include <functional>
+#include <system_error>
+#include <unistd.h>
+
+namespace fs = std::filesystem;
+using test::require;
+
+namespace
+{
+    int cases = 0;
+
+    // f must throw exactly E (or a subclass) whose what() contains `text`.
+    template <typename E>
+    void expect(const std::string &row, const std::function<void()> &f, const std::string &text)
+    {
+        ++cases;
+        try
+        {
+            f();
+        }
+        catch (const E &e)
+        {
+            const std::string what = e.what();
+            require(what.find(text) != std::string::npos,
+                    row + ": message \"" + what + "\" lacks \"" + text + "\"");
+            return;
+        }
+        catch (const std::exception &e)
+        {
+            throw std::runtime_error(row + ": wrong exception type, message \"" + e.what() + "\"");
+        }
+        throw std::runtime_error(row + ": no exception");
+    }
+
+    void accept(const std::string &row, const std::function<void()> &f)
+    {
+        ++cases;
+        try
+        {
+            f();
+        }
+        catch (const std::exception &e)
+        {
+            throw std::runtime_error(row + ": unexpected exception \"" + std::string(e.what()) + "\"");
+        }
+    }
+
+    fs::path scratch()
+    {
+        static const fs::path d = fs::temp_directory_path() / ("q3k_io_contract_" + std::to_string(::getpid()));
+        fs::create_directories(d);
+        return d;
+    }
+
+    void write_file(const fs::path &p, const std::string &bytes)
+    {
+        std::ofstream f(p, std::ios::binary | std::ios::trunc);
+        f.write(bytes.data(), static_cast<std::streamsize>(bytes.size()));
+    }
+
+    std::string framed(const std::string &header, const std::string &data, std::uint64_t length = ~0ULL)
+    {
+        const std::uint64_t n = length == ~0ULL ? header.size() : length;
+        std::string out(8, '\0');
+        for (int i = 0; i < 8; ++i)
+            out[static_cast<std::size_t>(i)] = static_cast<char>((n >> (8 * i)) & 0xff);
+        return out + header + data;
+    }
+
+    // A one-record header for tensor "a" over `data`.
+    std::string one(const std::string &record) { return "{\"a\":" + record + "}"; }
+
+    void open_metadata(const fs::path &p)
+    {
+        qwen3::SafetensorsFile f(p);
+        qwen3::SafetensorsMetadata m(f);
+    }
+
+    void file_rows()
+    {
+        const fs::path p = scratch() / "f.safetensors";
+        const auto bad = [&](const std::string &row, const std::string &bytes, const std::string &text) {
+            write_file(p, bytes);
+            expect<qwen3::SafetensorsFormatError>(row, [&] { qwen3::SafetensorsFile f(p); }, text);
+        };
+        bad("F1 shorter than the prefix", "1234567", "safetensors file is shorter than the 8-byte header length prefix: ");
+        bad("F2 empty header", framed("", ""), "safetensors header is empty: ");
+        bad("F3 header cap", framed("{}", "", 100000001ULL), "safetensors header exceeds 100,000,000 bytes: ");
+        bad("F4 header past the end", framed("{}", "", 3), "safetensors header extends beyond the end of the file: ");
+        bad("F5 no leading brace", framed(" {}", ""), "safetensors header must begin with '{': ");
+        expect<std::system_error>("MF1 missing file", [&] { qwen3::MappedFile m(scratch() / "absent"); }, "absent");
+        expect<std::invalid_argument>("MF2 not a regular file", [&] { qwen3::MappedFile m(scratch()); },
+                                      "mapped path is not a regular file: ");
+    }
+
+    void metadata_rows()
+    {
+        const fs::path p = scratch() / "m.safetensors";
+        const auto bad = [&](const std::string &row, const std::string &header, const std::string &data,
+                             const std::string &text) {
+            write_file(p, framed(header, data));
+            expect<qwen3::SafetensorsFormatError>(row, [&] { open_metadata(p); }, text);
+        };
+        const std::string d4 = "xxxx";
+        bad("M0 invalid JSON", "{\"a\":", d4, "invalid Safetensors JSON header: ");
+        bad("M0 trailing characters", "{} x", d4, "invalid Safetensors JSON header: ");
+        bad("M1 record not an object", one("[1]"), d4, "tensor 'a': metadata must be a JSON object");
+        bad("M2 missing data_offsets", one(R"({"dtype":"F32","shape":[1]})"), d4,
+            "tensor 'a': missing dtype, shape or data_offsets");
+        bad("M2 missing dtype", one(R"({"shape":[1],"data_offsets":[0,4]})"), d4, "missing dtype, shape or data_offsets");
+        bad("M3 dtype not a string", one(R"({"dtype":7,"shape":[1],"data_offsets":[0,4]})"), d4,
+            "tensor 'a': 'dtype' must be a string");
+        bad("M4 unsupported dtype", one(R"({"dtype":"F16","shape":[2],"data_offsets":[0,4]})"), d4,
+            "tensor 'a': unsupported dtype 'F16'");
+        bad("M5 shape not an array", one(R"({"dtype":"F32","shape":1,"data_offsets":[0,4]})"), d4,
+            "tensor 'a': 'shape' must be an array");
+        for (const char *dim : {"-1", "1.0", "1e0", "\"1\"", "18446744073709551616", "-0", "null"})
+            bad(std::string("M6 shape item ") + dim,
+                one(std::string(R"({"dtype":"F32","shape":[)") + dim + R"(],"data_offsets":[0,4]})"), d4,
+                "tensor 'a': 'shape' must contain unsigned integers");
+        bad("M7 dimension above int64", one(R"({"dtype":"F32","shape":[9223372036854775808],"data_offsets":[0,4]})"),
+            d4, "tensor 'a': 'shape' contains a value too large for a dimension");
+        for (const char *off : {"[0]", "[0,4,4]", "4", "{}"})
+            bad(std::string("M8 data_offsets ") + off,
+                one(std::string(R"({"dtype":"F32","shape":[1],"data_offsets":)") + off + "}"), d4,
+                "tensor 'a': 'data_offsets' must contain exactly two integers");
+        for (const char *off : {"[-1,4]", "[0,4.0]", "[0,\"4\"]"})
+            bad(std::string("M9 data_offsets ") + off,
+                one(std::string(R"({"dtype":"F32","shape":[1],"data_offsets":)") + off + "}"), d4,
+                "tensor 'a': 'data_offsets' must contain unsigned integers");
+        bad("M10 end before begin", one(R"({"dtype":"F32","shape":[1],"data_offsets":[4,0]})"), d4,
+            "tensor 'a': end offset is smaller than begin offset");
+        bad("M11 past the data", one(R"({"dtype":"F32","shape":[1],"data_offsets":[0,8]})"), d4,
+            "tensor 'a': data offset exceeds the weight data buffer");
+        bad("M12 element count overflow",
+            one(R"({"dtype":"F32","shape":[4294967296,4294967296],"data_offsets":[0,4]})"), d4,
+            "tensor 'a': shape element count overflow");
+        bad("M13 byte size overflow", one(R"({"dtype":"F32","shape":[4611686018427387904],"data_offsets":[0,4]})"),
+            d4, "tensor 'a': tensor byte size overflow");
+        bad("M14 size mismatch", one(R"({"dtype":"F32","shape":[2],"data_offsets":[0,4]})"), d4,
+            "tensor 'a': shape and data_offsets describe different byte sizes");
+        // rule order inside one record: the dtype rule runs before the shape rule
+        bad("M order dtype before shape", one(R"({"dtype":"X","shape":"no","data_offsets":[0,4]})"), d4,
+            "unsupported dtype 'X'");
+        // record order: the first failing record in name order
+        bad("M order by name",
+            R"({"b":{"dtype":"X","shape":[1],"data_offsets":[0,4]},"a":{"dtype":"F32","shape":[9],"data_offsets":[0,4]}})",
+            d4, "tensor 'a': shape and data_offsets describe different byte sizes");
+        // a JSON error anywhere wins over a bad record
+        bad("M order syntax first", R"({"a":{"dtype":"X","shape":[1],"data_offsets":[0,4]},"b":})", d4,
+            "invalid Safetensors JSON header: ");
+        // a repeated name keeps its last record
+        write_file(p, framed(R"({"a":{"dtype":"X"},"a":{"dtype":"I32","shape":[1],"data_offsets":[0,4]}})", d4));
+        accept("M repeated name keeps the last record", [&] {
+            qwen3::SafetensorsFile f(p);
+            qwen3::SafetensorsMetadata m(f);
+            require(m.tensor_count() == 1 && m.tensor("a").dtype == qwen3::DType::Int32, "last record kept");
+        });
+        // fields other than the three are ignored; a repeated field keeps its last value
+        write_file(p, framed(R"({"a":{"x":[{}],"dtype":"F16","dtype":"F32","shape":[1],"data_offsets":[0,4]},"__metadata__":{"k":[1,2]}})", d4));
+        accept("M unknown and repeated fields", [&] {
+            qwen3::SafetensorsFile f(p);
+            qwen3::SafetensorsMetadata m(f);
+            require(m.tensor("a").dtype == qwen3::DType::Float32, "last dtype kept");
+        });
+        write_file(p, framed(one(R"({"dtype":"I32","shape":[],"data_offsets":[0,4]})"), d4));
+        expect<std::out_of_range>("M15 unknown name", [&] {
+            qwen3::SafetensorsFile f(p);
+            qwen3::SafetensorsMetadata m(f);
+            (void)m.tensor("nope");
+        }, "Safetensors tensor not found: nope");
+        qwen3::SafetensorsLoader loader(p);
+        expect<std::out_of_range>("L1 unknown name in load", [&] { (void)loader.load("nope", qwen3::Device::cpu()); },
+                                  "Safetensors tensor not found: nope");
+        expect<std::out_of_range>("L1 unknown name in load_many",
+                                  [&] { (void)loader.load_many({"a", "nope"}, qwen3::Device::cpu()); },
+                                  "Safetensors tensor not found: nope");
+    }
+
+    // A directory with shards written from (name, dtype, shape, bytes) lists and an index text.
+    struct Tensor1
+    {
+        std::string name;
+        std::size_t floats;
+    };
+
+    void write_shard(const fs::path &p, const std::vector<Tensor1> &ts)
+    {
+        std::string header = "{", data;
+        for (std::size_t i = 0; i < ts.size(); ++i)
+        {
+            const std::size_t b = data.size(), e = b + 4 * ts[i].floats;
+            header += (i ? "," : "") + std::string("\"") + ts[i].name + "\":{\"dtype\":\"F32\",\"shape\":[" +
+                      std::to_string(ts[i].floats) + "],\"data_offsets\":[" + std::to_string(b) + "," +
+                      std::to_string(e) + "]}";
+            for (std::size_t k = 0; k < ts[i].floats; ++k)
+            {
+                const float v = static_cast<float>(i * 100 + k);
+                data.append(reinterpret_cast<const char *>(&v), 4);
+            }
+        }
+        write_file(p, framed(header + "}", data));
+    }
+
+    fs::path model_dir(const std::string &index)
+    {
+        const fs::path d = scratch() / "ckpt";
+        fs::remove_all(d);
+        fs::create_directories(d);
+        write_shard(d / "s1.safetensors", {{"w.a", 2}, {"w.b", 3}});
+        write_shard(d / "s2.safetensors", {{"w.c", 1}});
+        write_file(d / "model.safetensors.index.json", index);
+        return d;
+    }
+
+    const std::string kMap = R"("weight_map":{"w.a":"s1.safetensors","w.b":"s1.safetensors","w.c":"s2.safetensors"})";
+
+    void checkpoint_rows()
+    {
+        const auto bad = [&](const std::string &row, const std::string &index, const std::string &text) {
+            const fs::path d = model_dir(index);
+            expect<std::runtime_error>(row, [&] { qwen3::SafetensorsCheckpoint c(d); }, text);
+        };
+        accept("C good index", [&] {
+            qwen3::SafetensorsCheckpoint c(model_dir("{\"metadata\":{\"total_size\":24}," + kMap + "}"));
+            require(c.is_sharded() && c.shard_count() == 2 && c.tensor_count() == 3, "two shards, three tensors");
+            const auto ts = c.load_many({"w.c", "w.a", "w.c"}, qwen3::Device::cpu());
+            require(static_cast<const float *>(ts[1].data())[1] == 1.0F, "w.a values");
+            require(static_cast<const float *>(ts[0].data())[0] == 0.0F && ts[2].shape() == ts[0].shape(),
+                    "request order and repeated names");
+        });
+        expect<std::invalid_argument>("C1 no directory", [&] { qwen3::SafetensorsCheckpoint c(scratch() / "none"); },
+                                      "model directory does not exist: ");
+        {
+            const fs::path d = model_dir("{}");
+            write_shard(d / "model.safetensors", {{"x", 1}});
+            expect<std::runtime_error>("C2 both layouts", [&] { qwen3::SafetensorsCheckpoint c(d); },
+                                       "model directory contains both model.safetensors and model.safetensors.index.json");
+            fs::remove(d / "model.safetensors");
+            fs::remove(d / "model.safetensors.index.json");
+            expect<std::runtime_error>("C3 neither layout", [&] { qwen3::SafetensorsCheckpoint c(d); },
+                                       "model directory contains neither model.safetensors nor model.safetensors.index.json");
+            write_file(d / "model.safetensors", framed("{\"__metadata__\":{}}", ""));
+            expect<std::runtime_error>("C4 single file without tensors", [&] { qwen3::SafetensorsCheckpoint c(d); },
+                                       "single-file checkpoint contains no tensors");
+        }
+        bad("C6 invalid index JSON", "{\"metadata\":", "invalid checkpoint index '");
+        bad("C7 index root not an object", "[]", "checkpoint index root must be an object");
+        bad("C8 no metadata", "{" + kMap + "}", "checkpoint index must contain a metadata object");
+        bad("C8 metadata not an object", "{\"metadata\":3," + kMap + "}", "checkpoint index must contain a metadata object");
+        bad("C9 no total_size", "{\"metadata\":{}," + kMap + "}", "checkpoint metadata.total_size must be an unsigned integer");
+        bad("C9 negative total_size", "{\"metadata\":{\"total_size\":-24}," + kMap + "}",
+            "checkpoint metadata.total_size must be an unsigned integer");
+        bad("C10 no weight_map", "{\"metadata\":{\"total_size\":24}}", "checkpoint index weight_map must be a non-empty object");
+        bad("C10 empty weight_map", "{\"metadata\":{\"total_size\":24},\"weight_map\":{}}",
+            "checkpoint index weight_map must be a non-empty object");
+        bad("C11 entry not a string", R"({"metadata":{"total_size":24},"weight_map":{"w.a":1}})",
+            "checkpoint weight_map contains an invalid entry");
+        bad("C11 empty tensor name", R"({"metadata":{"total_size":24},"weight_map":{"":"s1.safetensors"}})",
+            "checkpoint weight_map contains an invalid entry");
+        for (const char *shard : {"", "../s1.safetensors", "a\\\\s1.safetensors", "s1.bin"})
+            bad(std::string("C12 shard name ") + shard,
+                std::string(R"({"metadata":{"total_size":24},"weight_map":{"w.a":")") + shard + "\"}}",
+                "invalid checkpoint shard name: ");
+        bad("C13 missing shard", R"({"metadata":{"total_size":24},"weight_map":{"w.a":"s9.safetensors"}})",
+            "checkpoint shard does not exist: ");
+        bad("C14 tensor missing from the index",
+            R"({"metadata":{"total_size":24},"weight_map":{"w.a":"s1.safetensors","w.c":"s2.safetensors"}})",
+            "tensor 'w.b' exists in a shard but not in the checkpoint index");
+        bad("C15 tensor in the wrong shard",
+            R"({"metadata":{"total_size":24},"weight_map":{"w.a":"s1.safetensors","w.b":"s2.safetensors","w.c":"s2.safetensors"}})",
+            "is stored in the wrong shard");
+        bad("C16 indexed tensor missing",
+            R"({"metadata":{"total_size":24},"weight_map":{"w.a":"s1.safetensors","w.b":"s1.safetensors","w.c":"s2.safetensors","w.z":"s2.safetensors"}})",
+            "indexed tensor is missing from its shard: w.z");
+        bad("C17 total_size mismatch", "{\"metadata\":{\"total_size\":25}," + kMap + "}",
+            "checkpoint total_size mismatch: expected 25, got 24");
+        {
+            const fs::path d = model_dir("{\"metadata\":{\"total_size\":24}," + kMap + "}");
+            qwen3::SafetensorsCheckpoint c(d);
+            expect<std::out_of_range>("C18 unknown name in tensor_info", [&] { (void)c.tensor_info("w.q"); },
+                                      "checkpoint tensor not found: w.q");
+            expect<std::out_of_range>("C18 unknown name in load", [&] { (void)c.load("w.q", qwen3::Device::cpu()); },
+                                      "checkpoint tensor not found: w.q");
+            expect<std::out_of_range>("C18 unknown name in load_many",
+                                      [&] { (void)c.load_many({"w.a", "w.q"}, qwen3::Device::cpu()); },
+                                      "checkpoint tensor not found: w.q");
+            write_shard(d / "s1.safetensors", {{"w.a", 3}, {"w.b", 2}});   // same names, other records
+            expect<std::runtime_error>("C19 shard rewritten after opening", [&] { (void)c.load("w.b", qwen3::Device::cpu()); },
+                                       "checkpoint changed while loading tensor: w.b");
+            expect<std::runtime_error>("C19 shard rewritten, load_many",
+                                       [&] { (void)c.load_many({"w.c", "w.a"}, qwen3::Device::cpu()); },
+                                       "checkpoint changed while loading tensor: w.a");
+        }
+    }
+
+    void json_rows()
+    {
+        using qwen3::io_detail::JsonCursor;
+        const auto parse = [](const std::string &text) {
+            JsonCursor c(text);
+            c.skip_value();
+            c.finish();
+        };
+        for (const char *ok : {"{}", "[]", " {\"a\" : [1, -2.5e+3, true, false, null, \"x\"] } ", "0", "-0", "1E5",
+                               "\"\\u00e9\\ud83d\\ude00\\n\\/\"", "[[[]]]", "\"\xc3\xa9\xe2\x82\xac\xf0\x9f\x98\x80\""})
+            accept(std::string("J valid ") + ok, [&] { parse(ok); });
+        for (const char *no : {"", "{", "{\"a\"}", "{\"a\":1,}", "[1,]", "[1 2]", "01", "1.", ".5", "1e", "+1", "tru",
+                               "nul", "\"\\x\"", "\"\\ud800\"", "\"\\udc00\"", "\"a", "{} {}", "{1:2}", "\"\x01\"",
+                               "\"\xc3\x28\"", "\"\xe0\x80\xaf\"", "\"\xed\xa0\x80\"", "\"\xf4\x90\x80\x80\"", "NaN"})
+            expect<std::runtime_error>(std::string("J invalid ") + no, [&] { parse(no); }, "JSON ");
+        accept("J decoded string", [&] {
+            JsonCursor c("\"t\\u00e9\\n\\ud83d\\ude00\"");
+            require(c.read_string() == "t\xc3\xa9\n\xf0\x9f\x98\x80", "escapes decoded to UTF-8");
+        });
+        accept("J numbers", [&] {
+            JsonCursor c("[18446744073709551615, 18446744073709551616, 0, -0, 3.0]");
+            c.open_array();
+            std::vector<JsonCursor::Number> n;
+            while (c.next_item())
+                n.push_back(c.read_number());
+            require(n.size() == 5 && n[0].is_unsigned && n[0].value == 18446744073709551615ULL, "u64 max");
+            require(!n[1].is_unsigned && n[2].is_unsigned && !n[3].is_unsigned && !n[4].is_unsigned, "kinds");
+        });
+        std::string deep(300, '[');
+        deep += std::string(300, ']');
+        expect<std::runtime_error>("J nesting limit", [&] { parse(deep); }, "nesting too deep");
+    }
+
+    void body()
+    {
+        file_rows();
+        metadata_rows();
+        checkpoint_rows();
+        json_rows();
+        fs::remove_all(scratch());
+        std::cout << cases << " contract cases\n";
+    }
+} // namespace
+
+int main() { return test::run("safetensors IO contract (CPU) test", body); }
