@@ -46,6 +46,18 @@ namespace q3k
         return r;
     }
 
+    // NT = true: a streaming store with device scope (`nt sc1`).  The eight
+    // XCDs of MI355X each have their own L2, and a store at device scope is
+    // written through it instead of leaving a dirty line that the end of the
+    // kernel has to write back before the next kernel may start.  Measured on
+    // a 64 MB -> 64 MB copy: 72.8% of peak HBM with `nt` alone, 76.1% with
+    // `nt sc1`.  No compiler builtin sets sc1 on a global store, hence the
+    // asm.  A 128-bit store reads its data VGPRs a few cycles after it
+    // issues, and a VALU write to them in that window corrupts the store; for
+    // its own stores the compiler keeps such a write two wait states back
+    // (`s_nop 1`), but it cannot see into the asm, so the asm carries those
+    // wait states itself.  A store returns nothing, so there is no counter
+    // wait for the compiler to track.
     template <bool NT>
     __device__ __forceinline__ void store8(Vec8 *p, const Vec8 &r)
     {
@@ -55,7 +67,7 @@ namespace q3k
         v.z = r.d[2];
         v.w = r.d[3];
         if constexpr (NT)
-            __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p));
+            __asm__ volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
         else
             *reinterpret_cast<u32x4 *>(p) = v;
     }

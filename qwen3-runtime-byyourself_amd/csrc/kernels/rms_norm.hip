@@ -99,8 +99,11 @@ namespace q3k
             return partial;
         }
 
-        // Loads of one row slice: x (and d) from their rows, the weights.
-        template <int VPT, int MODE, int NTM>
+        // Loads of one row slice: every x vector first, then d (add mode),
+        // then the weights (issuing the HBM streams ahead of the weight reads,
+        // which hit the cache, measured faster).  FULL: the slice covers the
+        // row exactly, so no vector needs a bounds test.
+        template <int VPT, int MODE, int NTM, bool FULL>
         __device__ __forceinline__ void load_row(const Vec8 *src, const uint16_t *d, const RowMap &map, int64_t out_row,
                                                  int nvec, const Vec8 *wvec, int first_vec, int vec_step, Vec8 (&x)[VPT],
                                                  Vec8 (&dv)[VPT], Vec8 (&wv)[VPT], bool (&live)[VPT])
@@ -108,24 +111,34 @@ namespace q3k
             const Vec8 zero = {{0u, 0u, 0u, 0u}};
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
+                live[i] = FULL || first_vec + i * vec_step < nvec;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
             {
-                const int j = first_vec + i * vec_step;
-                live[i] = j < nvec;
                 if (!live[i])
                     continue;
+                const int j = first_vec + i * vec_step;
                 if constexpr (MODE == kGatherNorm)
                     x[i] = src != nullptr ? load8<false>(src + j) : zero;
                 else
                     x[i] = load8<nt_load(NTM)>(src + j);
-                if constexpr (MODE == kAddNorm)
-                    dv[i] = load8<nt_load(NTM)>(reinterpret_cast<const Vec8 *>(d) +
-                                                (map.first + out_row * map.stride) * nvec + j);
-                wv[i] = wvec[j];
             }
+            if constexpr (MODE == kAddNorm)
+            {
+                const Vec8 *drow = reinterpret_cast<const Vec8 *>(d) + (map.first + out_row * map.stride) * nvec;
+#pragma unroll
+                for (int i = 0; i < VPT; ++i)
+                    if (live[i])
+                        dv[i] = load8<nt_load(NTM)>(drow + first_vec + i * vec_step);
+            }
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (live[i])
+                    wv[i] = wvec[first_vec + i * vec_step];
         }
 
         // Group of G lanes per row (G <= 64), VPT vectors per lane.
-        template <int G, int VPT, int MODE, int NTM>
+        template <int G, int VPT, int MODE, int NTM, bool FULL>
         __global__ __launch_bounds__(kBlock) void rms_rows_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
@@ -139,8 +152,8 @@ namespace q3k
 
             Vec8 x[VPT], dv[VPT], wv[VPT];
             bool live[VPT];
-            load_row<VPT, MODE, NTM>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
-                                     reinterpret_cast<const Vec8 *>(w), lane, G, x, dv, wv, live);
+            load_row<VPT, MODE, NTM, FULL>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
+                                           reinterpret_cast<const Vec8 *>(w), lane, G, x, dv, wv, live);
             const float partial = add_and_square<VPT, MODE>(x, dv, live);
             if constexpr (MODE != kNorm)
             {
@@ -161,7 +174,7 @@ namespace q3k
         // One row per block of WPR waves, VPT vectors per lane; the wave sums
         // meet in LDS behind one barrier.  PR > 0 raises the wave priority
         // while the loads are issued.
-        template <int WPR, int VPT, int MODE, int NTM, int PR, bool REMAP>
+        template <int WPR, int VPT, int MODE, int NTM, int PR, bool REMAP, bool FULL>
         __global__ __launch_bounds__(WPR * kWave) void rms_block_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
@@ -176,8 +189,8 @@ namespace q3k
             bool live[VPT];
             if constexpr (PR > 0)
                 __builtin_amdgcn_s_setprio(PR);
-            load_row<VPT, MODE, NTM>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
-                                     reinterpret_cast<const Vec8 *>(w), t, kThreads, x, dv, wv, live);
+            load_row<VPT, MODE, NTM, FULL>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
+                                           reinterpret_cast<const Vec8 *>(w), t, kThreads, x, dv, wv, live);
             if constexpr (PR > 0)
                 __builtin_amdgcn_s_setprio(0);
 
@@ -290,9 +303,12 @@ namespace q3k
         constexpr int ntm_block() { return MODE == kGatherNorm ? 2 : 3; }
         template <int MODE>
         constexpr int ntm_rows() { return MODE == kNorm ? 2 : MODE == kAddNorm ? 3 : 2; }
-        // Wave priority raised while loads are issued (measured: helps the fused add).
+        // Wave priority while the loads are issued: raised priority helped the
+        // fused add while stores were written back from L2 at the end of each
+        // kernel; with write-through stores the default is faster (77.7%
+        // against 76.3% of peak for add + norm at T = 8192, H = 4096).
         template <int MODE>
-        constexpr int prio_block() { return MODE == kAddNorm ? 1 : 0; }
+        constexpr int prio_block() { return 0; }
         constexpr bool kRemapRows = false;  // XCD-contiguous rows measured slower
 
         struct Launch
@@ -313,17 +329,25 @@ namespace q3k
         void launch_rows(const Launch &l)
         {
             constexpr int kRowsPerBlock = kBlock / G;
-            const int64_t blocks = (l.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-            rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>()><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, l.stream>>>(
-                l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            const dim3 grid(static_cast<unsigned>((l.rows + kRowsPerBlock - 1) / kRowsPerBlock));
+            if (l.nvec == G * VPT)
+                rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), true><<<grid, dim3(kBlock), 0, l.stream>>>(
+                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            else
+                rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), false><<<grid, dim3(kBlock), 0, l.stream>>>(
+                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
         }
 
         template <int WPR, int VPT, int MODE>
         void launch_block(const Launch &l)
         {
-            rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows>
-                <<<dim3(static_cast<unsigned>(l.rows)), dim3(WPR * kWave), 0, l.stream>>>(
-                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            const dim3 grid(static_cast<unsigned>(l.rows)), block(WPR * kWave);
+            if (l.nvec == WPR * kWave * VPT)
+                rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, true>
+                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            else
+                rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, false>
+                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
         }
 
         template <int VPT, int MODE>
@@ -348,8 +372,10 @@ namespace q3k
         //                 (per-head norms, 128 elements = 16 lanes);
         //   nvec <= 128:  one wave per row, 1-2 vectors per lane (hidden 1024);
         //   nvec <= 2048: one row per block of up to 8 waves; one vector per lane
-        //                 for the fused add and the gather when nvec <= 512
-        //                 (hidden <= 4096), else two (four beyond 8192 elements).
+        //                 when nvec <= 512 (hidden <= 4096), else two (four
+        //                 beyond 8192 elements).  One vector per lane streams
+        //                 fastest (a 64 MB row copy: 76.4% of peak with one,
+        //                 73.7% with two, 70.8% with eight).
         template <int MODE>
         bool launch_fast(const Launch &l)
         {
@@ -370,7 +396,7 @@ namespace q3k
                 launch_rows<64, 1, MODE>(l);
             else if (nvec <= 128)
                 launch_rows<64, 2, MODE>(l);
-            else if (MODE != kNorm && nvec <= 512)
+            else if (nvec <= 512)
                 return launch_block_waves<1, MODE>((nvec + 63) / 64, l);
             else if (nvec <= 1024)
                 return launch_block_waves<2, MODE>((nvec + 127) / 128, l);

@@ -41,6 +41,11 @@ namespace q3k
         constexpr int kNtmRope = 3;
         constexpr int kNtmNormRope = 3;
         constexpr bool kRemapHeads = false;  // XCD-contiguous tiles measured slower
+        // Wave priority while the head loads are issued.  Raising it helped
+        // while stores were written back from L2 at the end of each kernel;
+        // with write-through stores the default is faster (c4: 77.0%
+        // against 75.6% of peak with priority 3; c5: 82.9% against 81.7%).
+        constexpr int kPrioHeads = 0;
 
         struct RopeShape
         {
@@ -86,17 +91,15 @@ namespace q3k
         // pattern and the norm weights depend only on the lane and the
         // position, so they are loaded and unpacked once per wave.  With
         // COPY_V the wave also moves the matching V heads from vsrc to vdst.
-        template <bool NORM, int NTM, int HG, bool COPY_V>
+        template <bool NORM, int NTM, int HG, bool COPY_V, int PR>
         __device__ __forceinline__ void rope_heads(const Vec8 *src, Vec8 *dst, const Vec8 *vsrc, Vec8 *vdst,
                                                    const uint16_t *w, const float *table, int64_t pos, float eps)
         {
             const int lane16 = threadIdx.x % 16;
-            // Raised wave priority while the head loads are issued gets them
-            // to the memory system ahead of other waves' arithmetic (+5%
-            // measured at the model's shapes).
             Vec8 x[HG];
             Vec8 xv[COPY_V ? HG : 1];
-            __builtin_amdgcn_s_setprio(3);
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(PR);
 #pragma unroll
             for (int i = 0; i < HG; ++i)
                 x[i] = load8<nt_load(NTM)>(src + i * kHeadStride);
@@ -106,7 +109,8 @@ namespace q3k
                 for (int i = 0; i < HG; ++i)
                     xv[i] = load8<nt_load(NTM)>(vsrc + i * kHeadStride);
             }
-            __builtin_amdgcn_s_setprio(0);
+            if constexpr (PR > 0)
+                __builtin_amdgcn_s_setprio(0);
 
             if (pos < 0)
             {
@@ -209,7 +213,7 @@ namespace q3k
         // HGK.  Q is rewritten in place; K in place too, or with KV into the
         // cache rows given by `kv` (k itself is then only read).  Heads and
         // tokens are wave-uniform and below 2^31 (checked by the launcher).
-        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV>
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
@@ -225,7 +229,7 @@ namespace q3k
                 const uint32_t head0 = static_cast<uint32_t>(wave * kHeadsPerWave * HGQ);
                 const uint32_t token = head0 / static_cast<uint32_t>(heads_q);
                 Vec8 *p = reinterpret_cast<Vec8 *>(q) + lane_vec(head0);
-                rope_heads<NORM, NTM, HGQ, false>(p, p, nullptr, nullptr, qw, rs.cache, token_position(rs, token),
+                rope_heads<NORM, NTM, HGQ, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, token_position(rs, token),
                                                   eps);
                 return;
             }
@@ -239,14 +243,14 @@ namespace q3k
                 const uint32_t b = token / seq;
                 const int64_t row = static_cast<int64_t>(b) * kv.seq_cap + kv.cache_start + (token - b * seq);
                 const int64_t dst_head = row * heads_k + (head0 - token * static_cast<uint32_t>(heads_k));
-                rope_heads<NORM, NTM, HGK, true>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + lane_vec(dst_head),
+                rope_heads<NORM, NTM, HGK, true, PR>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + lane_vec(dst_head),
                                                  reinterpret_cast<const Vec8 *>(kv.v) + lane_vec(head0),
                                                  reinterpret_cast<Vec8 *>(kv.v_cache) + lane_vec(dst_head), kw,
                                                  rs.cache, pos, eps);
             }
             else
             {
-                rope_heads<NORM, NTM, HGK, false>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
+                rope_heads<NORM, NTM, HGK, false, PR>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
             }
         }
 
@@ -345,7 +349,7 @@ namespace q3k
             const int64_t q_waves = waves_for(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
+            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
                 q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
