@@ -1,7 +1,9 @@
 #pragma once
 
 // Owning, move-only byte storage on the host (64-byte aligned) or on a GPU
-// (hipMalloc).  Contract pinned by the reference's tests/unit/buffer_cpu_test.cpp
+// (hipMalloc; device blocks of at most 4 MiB are kept for reuse when their
+// Buffer is destroyed, in the order of the default stream, up to 64 MiB per
+// device).  Contract pinned by the reference's tests/unit/buffer_cpu_test.cpp
 // and buffer_cuda_test.cpp: zero bytes give a null pointer, a moved-from
 // buffer is empty, copies check sizes (std::invalid_argument) and ranges
 // (std::out_of_range), GPU allocation failures throw std::runtime_error and
@@ -10,6 +12,7 @@
 #include "qwen3/core/device.h"
 
 #include <cstddef>
+#include <cstdint>
 
 namespace qwen3
 {
@@ -40,6 +43,13 @@ namespace qwen3
         std::size_t size_bytes_;
         Device device_;
     };
+
+    // Device allocations (hipMalloc calls) made by Buffers in this process;
+    // a block taken from the reuse cache does not count.
+    [[nodiscard]] std::uint64_t device_allocation_count() noexcept;
+
+    // Frees the device blocks kept for reuse (every GPU).
+    void release_cached_device_blocks();
 
     // Whole-buffer copy between any two devices (synchronous).
     void copy_buffer(Buffer &destination, const Buffer &source);

@@ -1,6 +1,7 @@
 // Pinned, chunked host -> GPU upload (see staged_upload.hpp).
 #include "staged_upload.hpp"
 
+#include "../core/block_cache.hpp"
 #include "qwen3/hip/hip_check.h"
 #include "qwen3/io/copy_crew.h"
 
@@ -39,7 +40,6 @@ namespace qwen3::io_detail
         try
         {
             QWEN3_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
-            QWEN3_HIP_CHECK(hipEventCreateWithFlags(&queued_before_, hipEventDisableTiming));
             for (std::size_t s = 0; s < kSlots; ++s)
             {
                 QWEN3_HIP_CHECK(hipHostMalloc(&slot_[s], kSlotBytes, hipHostMallocDefault));
@@ -71,11 +71,8 @@ namespace qwen3::io_detail
             slot_done_[s] = nullptr;
             slot_[s] = nullptr;
         }
-        if (queued_before_ != nullptr)
-            (void)hipEventDestroy(queued_before_);
         if (stream_ != nullptr)
             (void)hipStreamDestroy(stream_);
-        queued_before_ = nullptr;
         stream_ = nullptr;
         if (restore)
             (void)hipSetDevice(previous);
@@ -85,6 +82,9 @@ namespace qwen3::io_detail
                            const std::function<UploadPiece(std::size_t)> &piece)
     {
         hip::DeviceGuard guard(device_);
+        // destinations made by piece() are fresh memory, which no work queued
+        // on another stream can still be reading
+        const qwen3::detail::FreshDeviceBlocks fresh;
         detail::CopyCrew crew(crew_helpers(total_bytes));
         // the slot being filled: host segments to copy into it, and where its bytes land
         std::size_t slot = 0, used = 0;
@@ -110,8 +110,6 @@ namespace qwen3::io_detail
 
         try
         {
-            QWEN3_HIP_CHECK(hipEventRecord(queued_before_, nullptr));
-            QWEN3_HIP_CHECK(hipStreamWaitEvent(stream_, queued_before_, 0));
             for (std::size_t i = 0; i < count; ++i)
             {
                 const UploadPiece p = piece(i);
