@@ -227,6 +227,20 @@ Q3K_API int q3k_argmax_bf16(const uint16_t *x, int32_t *out, int64_t rows,
 Q3K_API int64_t q3k_argmax_workspace_bytes(int64_t rows, int64_t search_size);
 
 /*
+ * q3k_argmax_bf16 for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops): the same result, with the slice
+ * results in a fixed 16 KiB array in device memory that the library holds on
+ * each GPU it runs on until the process ends, instead of a caller
+ * workspace.  Every input fits it (slicing needs fewer than 8 KiB); a plan
+ * needing more returns Q3K_ERR_INVALID_ARGUMENT.  The call itself allocates
+ * nothing.  Calls on one GPU share that array, so calls that overlap on one
+ * GPU race.  No counterpart in the reference.
+ */
+Q3K_API int q3k_argmax_bf16_noalloc(const uint16_t *x, int32_t *out, int64_t rows,
+                  int64_t row_stride, int64_t search_size,
+                  q3k_stream_t stream);
+
+/*
  * Top-k candidates of sampling.  For each row r of logits (bf16, row_stride
  * columns, the first search_size searched): every token whose logit is >=
  * the k-th largest logit (ties at the k-th all kept; -0 equals +0), written

@@ -84,6 +84,7 @@ SIGNATURES = {
     "q3k_gqa_attention_workspace_bytes": [_i64, _i64, _i32, _i32, _i32, _i64],
     "q3k_argmax_bf16": [_p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "q3k_argmax_workspace_bytes": [_i64, _i64],
+    "q3k_argmax_bf16_noalloc": [_p, _p, _i64, _i64, _i64, _p],
     "q3k_topk_candidates_bf16": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _i64, _p],
     "q3k_topk_workspace_bytes": [_i64, _i64, _i32],
     "q3k_kv_append": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
@@ -207,6 +208,10 @@ def gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, cached):
 def argmax(x, out, rows, row_stride, search_size, stream=None, workspace=None, workspace_bytes=0):
     _check(load().q3k_argmax_bf16(_ptr(x), _ptr(out), rows, row_stride, search_size, _ptr(workspace),
                                   workspace_bytes, _ptr(stream)))
+
+
+def argmax_noalloc(x, out, rows, row_stride, search_size, stream=None):
+    _check(load().q3k_argmax_bf16_noalloc(_ptr(x), _ptr(out), rows, row_stride, search_size, _ptr(stream)))
 
 
 def argmax_workspace_bytes(rows, search_size):

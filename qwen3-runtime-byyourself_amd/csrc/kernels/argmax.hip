@@ -15,6 +15,8 @@
 // order is total, so the result is the same).
 #include "q3k_common.hpp"
 
+#include <mutex>
+
 namespace q3k
 {
     namespace
@@ -186,53 +188,143 @@ namespace q3k
     } // namespace
 } // namespace q3k
 
+namespace q3k
+{
+    namespace
+    {
+        // Shared checks of both argmax entry points (src/ops/argmax.cu:104-161).
+        int validate_argmax(const uint16_t *x, const int32_t *out, int64_t rows, int64_t row_stride,
+                            int64_t search_size)
+        {
+            if (rows < 0)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax row count cannot be negative");
+            if (row_stride <= 0)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax reduction dimension must be positive");
+            if (row_stride > INT32_MAX)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax reduction dimension exceeds Int32 index range");
+            if (search_size <= 0 || search_size > row_stride)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "valid reduction size is outside the last dimension");
+            if (rows == 0)
+                return Q3K_OK;
+            if (x == nullptr || out == nullptr)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax received a null pointer");
+            if (!aligned_to(x, 2) || !aligned_to(out, 4))
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax pointers must be aligned to their element size");
+            if (rows > INT64_MAX / row_stride)
+                return set_error(Q3K_ERR_OVERFLOW, "argmax input size overflows");
+            return Q3K_OK;
+        }
+
+        // Launches for checked arguments: the sliced kernels when `part`
+        // (8-byte aligned, room for plan.bytes) is given and the plan slices,
+        // else one block per row.
+        int launch_argmax(const uint16_t *x, int32_t *out, int64_t rows, int64_t row_stride, int64_t search_size,
+                          const SlicePlan &plan, uint64_t *part, hipStream_t s)
+        {
+            const bool vec = aligned16(x) && row_stride % 8 == 0;
+            if (plan.slices > 1 && part != nullptr)
+            {
+                const dim3 grid(static_cast<unsigned>(rows * plan.slices));
+                if (vec)
+                    argmax_slice_kernel<true><<<grid, dim3(kArgmaxBlock), 0, s>>>(x, part, row_stride, search_size,
+                                                                                  plan.slices, plan.slice_len);
+                else
+                    argmax_slice_kernel<false><<<grid, dim3(kArgmaxBlock), 0, s>>>(x, part, row_stride, search_size,
+                                                                                   plan.slices, plan.slice_len);
+                const int64_t per_block = kBlock / kWave;
+                argmax_merge_kernel<<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)), dim3(kBlock), 0,
+                                      s>>>(part, out, rows, plan.slices);
+                return check_launch("argmax_last_dimension");
+            }
+            const unsigned grid = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+            if (vec)
+                argmax_kernel<true><<<dim3(grid), dim3(kArgmaxBlock), 0, s>>>(x, out, rows, row_stride, search_size);
+            else
+                argmax_kernel<false><<<dim3(grid), dim3(kArgmaxBlock), 0, s>>>(x, out, rows, row_stride, search_size);
+            return check_launch("argmax_last_dimension");
+        }
+
+        // The slice results of q3k_argmax_bf16_noalloc: a fixed array in
+        // device memory, one copy per GPU, held until the process ends.  The
+        // slice plan needs rows * slices * 8 bytes with rows * slices < 1024
+        // (rows < 512, slices <= ceil(512 / rows)), so 8 KiB covers every
+        // input; the array has twice that.  Every entry a call reads is
+        // written by the same call first, so nothing needs clearing.
+        constexpr int64_t kArgmaxScratchBytes = 16384;
+        constexpr int kMaxScratchDevices = 64;
+        std::mutex g_scratch_mutex;
+        void *g_scratch_address[kMaxScratchDevices];  // per device, from hipGetSymbolAddress
+    } // namespace
+
+    static __device__ __align__(256) uint64_t scratch[kArgmaxScratchBytes / sizeof(uint64_t)];
+
+    namespace
+    {
+        // The device address of `scratch` on the current GPU, looked up on
+        // the first call per GPU (the host-side name is not a device address).
+        int scratch_address(void **address)
+        {
+            int device = 0;
+            if (hipGetDevice(&device) != hipSuccess)
+                return set_error(Q3K_ERR_HIP, "argmax: no current GPU");
+            if (device < 0 || device >= kMaxScratchDevices)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax scratch supports GPUs 0 .. %d", kMaxScratchDevices - 1);
+            std::lock_guard<std::mutex> lock(g_scratch_mutex);
+            if (g_scratch_address[device] == nullptr)
+            {
+                void *p = nullptr;
+                const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+                if (e != hipSuccess || p == nullptr)
+                    return set_error(Q3K_ERR_HIP, "argmax scratch lookup failed on GPU %d: %s", device,
+                                     hipGetErrorString(e));
+                g_scratch_address[device] = p;
+            }
+            *address = g_scratch_address[device];
+            return Q3K_OK;
+        }
+    } // namespace
+} // namespace q3k
+
 extern "C" int q3k_argmax_bf16(const uint16_t *x, int32_t *out, int64_t rows, int64_t row_stride,
                                int64_t search_size, void *workspace, int64_t workspace_bytes,
                                q3k_stream_t stream)
 {
     using namespace q3k;
-    if (rows < 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax row count cannot be negative");
-    if (row_stride <= 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax reduction dimension must be positive");
-    if (row_stride > INT32_MAX)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax reduction dimension exceeds Int32 index range");
-    if (search_size <= 0 || search_size > row_stride)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "valid reduction size is outside the last dimension");
+    if (const int st = validate_argmax(x, out, rows, row_stride, search_size))
+        return st;
     if (workspace_bytes < 0)
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax workspace size cannot be negative");
     if (rows == 0)
         return Q3K_OK;
-    if (x == nullptr || out == nullptr)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax received a null pointer");
-    if (!aligned_to(x, 2) || !aligned_to(out, 4))
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "argmax pointers must be aligned to their element size");
-    if (rows > INT64_MAX / row_stride)
-        return set_error(Q3K_ERR_OVERFLOW, "argmax input size overflows");
-    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const bool vec = aligned16(x) && row_stride % 8 == 0;
     const SlicePlan plan = plan_slices(rows, search_size);
-    if (plan.slices > 1 && workspace != nullptr && workspace_bytes >= plan.bytes && aligned_to(workspace, 8))
+    const bool sliced = plan.slices > 1 && workspace != nullptr && workspace_bytes >= plan.bytes &&
+                        aligned_to(workspace, 8);
+    return launch_argmax(x, out, rows, row_stride, search_size, plan,
+                         sliced ? static_cast<uint64_t *>(workspace) : nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int q3k_argmax_bf16_noalloc(const uint16_t *x, int32_t *out, int64_t rows, int64_t row_stride,
+                                       int64_t search_size, q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_argmax(x, out, rows, row_stride, search_size))
+        return st;
+    if (rows == 0)
+        return Q3K_OK;
+    const SlicePlan plan = plan_slices(rows, search_size);
+    uint64_t *part = nullptr;
+    if (plan.slices > 1)
     {
-        uint64_t *part = static_cast<uint64_t *>(workspace);
-        const dim3 grid(static_cast<unsigned>(rows * plan.slices));
-        if (vec)
-            argmax_slice_kernel<true><<<grid, dim3(kArgmaxBlock), 0, s>>>(x, part, row_stride, search_size,
-                                                                          plan.slices, plan.slice_len);
-        else
-            argmax_slice_kernel<false><<<grid, dim3(kArgmaxBlock), 0, s>>>(x, part, row_stride, search_size,
-                                                                           plan.slices, plan.slice_len);
-        const int64_t per_block = kBlock / kWave;
-        argmax_merge_kernel<<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)), dim3(kBlock), 0, s>>>(
-            part, out, rows, plan.slices);
-        return check_launch("argmax_last_dimension");
+        if (plan.bytes > kArgmaxScratchBytes)
+            return set_error(Q3K_ERR_INVALID_ARGUMENT,
+                             "argmax needs %lld bytes of scratch, more than the library's fixed %lld",
+                             static_cast<long long>(plan.bytes), static_cast<long long>(kArgmaxScratchBytes));
+        void *address = nullptr;
+        if (const int st = scratch_address(&address))
+            return st;
+        part = static_cast<uint64_t *>(address);
     }
-    const unsigned grid = static_cast<unsigned>(rows < 65535 ? rows : 65535);
-    if (vec)
-        argmax_kernel<true><<<dim3(grid), dim3(kArgmaxBlock), 0, s>>>(x, out, rows, row_stride, search_size);
-    else
-        argmax_kernel<false><<<dim3(grid), dim3(kArgmaxBlock), 0, s>>>(x, out, rows, row_stride, search_size);
-    return check_launch("argmax_last_dimension");
+    return launch_argmax(x, out, rows, row_stride, search_size, plan, part, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t q3k_argmax_workspace_bytes(int64_t rows, int64_t search_size)
