@@ -85,6 +85,8 @@ def make_chain_set(hip, synth, configs, c, q3k, seed_shift=0):
         "o": hip.DeviceBuffer(T * I * 2),
         "cache": DB(q3k.build_rope_cache(c.max_pos, D, configs.THETA)),
     }
+    if c.positions == "uniform":   # one position per sequence (config 3): the Int32 positions overload
+        bufs["pos"] = DB(synth.uniform_positions(s, configs.TID_POS, T, c.max_pos))
     return bufs
 
 
@@ -102,7 +104,7 @@ def chain_ops(q3k, c, b, stream):
     return [
         ("add_rms_norm_attn", lambda: q3k.add_rms_norm(b["h1"], b["d1"], b["w1"], b["y1"], T, H, EPS, stream)),
         ("qk_norm_rope", lambda: q3k.qk_norm_rope(b["q"], b["k"], b["qw"], b["kw"], c.batch, c.seq, c.heads_q,
-                                                  c.heads_kv, D, EPS, b["cache"], c.max_pos, 0, None, stream)),
+                                                  c.heads_kv, D, EPS, b["cache"], c.max_pos, 0, b.get("pos"), stream)),
         ("add_rms_norm_mlp", lambda: q3k.add_rms_norm(b["h2"], b["d2"], b["w2"], b["y2"], T, H, EPS, stream)),
         ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * c.inter, stream)),
     ]
@@ -300,26 +302,80 @@ def time_sampling(q3k, hip, synth, configs, c, stream):
     return out
 
 
+TRAFFIC_PROFILE = os.path.join("profiles", "pmc_traffic_c4.md")
+
+
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) over the kernel sources, in name order: a rocprof summary records the hash
+    of the sources it measured, so a line can tell whether its traffic figure still describes these kernels."""
+    import hashlib
+    kdir = os.path.join(REPO, PKG, "csrc", "kernels")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(kdir)):
+        if name.endswith((".hip", ".hpp")):
+            h.update(name.encode())
+            with open(os.path.join(kdir, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def read_traffic(kernel_key):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
-    path = os.path.join(REPO, "profiles", "pmc_traffic_c4.md")
+    """HBM bytes per launch of `kernel_key` from the committed rocprofv3 --pmc summary, and where the figure
+    comes from: the file, the commit and kernel-source hash it records, and whether that hash is the one of
+    the kernels this run measured (if not, the figure is stale)."""
+    path = os.path.join(REPO, TRAFFIC_PROFILE)
+    source = {"file": TRAFFIC_PROFILE, "commit": None, "kernel_sources": None, "current_kernel_sources":
+              kernel_source_hash(), "stale": True}
     if not os.path.exists(path):
-        return None
+        return None, source
+    value = None
     with open(path) as f:
         for line in f:
-            parts = line.strip().strip("|").split("|")
+            text = line.strip()
+            if text.startswith("Generated at commit"):
+                source["commit"] = text.split()[-1].strip("`.")
+            elif text.startswith("Kernel sources sha256/16"):
+                source["kernel_sources"] = text.split()[-1].strip("`.")
+            parts = text.strip("|").split("|")
             if len(parts) >= 2 and parts[0].strip() == kernel_key:
                 try:
-                    return int(float(parts[-1].strip()))
+                    value = int(float(parts[-1].strip()))
                 except ValueError:
-                    return None
-    return None
+                    pass
+    source["stale"] = source["kernel_sources"] != source["current_kernel_sources"]
+    return value, source
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every core this process may run on (its CPU affinity), within the job's
+    CPU share when the environment states one (OMP_NUM_THREADS, set on the GPU boxes)."""
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except AttributeError:
+        visible = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    used = min(visible, int(share)) if share.isdigit() and int(share) > 0 else visible
+    return max(1, used), visible
 
 
 def cpu_baseline(configs, synth, seconds):
-    """The oracle (a C restatement of the reference's CPU arithmetic) on a
-    bounded sample of the config-4 chain: the same four ops over the first
-    Ts tokens, repeated until `seconds` elapse, on all host cores and on one."""
+    """The oracle (a C restatement of the reference's CPU arithmetic, worker threads kept for the whole run) on
+    bounded samples of the benchmark configs, on all the job's cores and on one:
+      - the config-4 chain (add_rms_norm x2, qk_norm_rope on Q with q_norm and K with k_norm, silu_mul) over
+        its first Ts tokens, repeated until its share of `seconds` has elapsed;
+      - config 1 itself (RMSNorm [16, 1024]), with the reference test's own CPU loop
+        (tests/unit/rms_norm_cuda_test.cpp:174-244)."""
     spec = importlib.util.spec_from_file_location("q3k_oracle", os.path.join(REPO, "oracle", "q3k_oracle.py"))
     oracle = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(oracle)
@@ -331,41 +387,53 @@ def cpu_baseline(configs, synth, seconds):
     q = synth.normal_bf16(c.seed, configs.TID_Q, (1, Ts, c.heads_q * D))
     k = synth.normal_bf16(c.seed, configs.TID_K, (1, Ts, c.heads_kv * D))
     qw = synth.normal_bf16(c.seed, configs.TID_QW, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(c.seed, configs.TID_KW, (D,), mean=1.0, std=0.1)
     g = synth.normal_bf16(c.seed, configs.TID_GATE, (Ts, I))
     u = synth.normal_bf16(c.seed, configs.TID_UP, (Ts, I))
     cache = oracle.build_rope_cache(Ts, D, configs.THETA)
     nbytes = configs.chain_bytes(configs.Config("sample", 0, 1, Ts, H, I, c.heads_q, c.heads_kv, "range", Ts))
+    c1 = configs.CONFIGS["c1"]
+    x1 = synth.normal_bf16(c1.seed, configs.TID_X, (c1.seq, c1.hidden))
+    wf1 = synth.normal_bf16(c1.seed, configs.TID_WF, (c1.hidden,), mean=1.0, std=0.1)
+    c1_bytes = configs.bytes_rms_norm(c1.tokens, c1.hidden)
 
-    def one_pass(nt):
+    def chain_pass(nt):
         oracle.add_rms_norm(h1, d1, w1, EPS, band=False, nthreads=nt)
         oracle.qk_norm_rope(q, qw, 1, Ts, c.heads_q, D, EPS, cache, band=False, nthreads=nt)
-        oracle.qk_norm_rope(k, qw, 1, Ts, c.heads_kv, D, EPS, cache, band=False, nthreads=nt)
+        oracle.qk_norm_rope(k, kw, 1, Ts, c.heads_kv, D, EPS, cache, band=False, nthreads=nt)
         oracle.add_rms_norm(h1, d1, w1, EPS, band=False, nthreads=nt)
         oracle.silu_mul(g, u, band=False, nthreads=nt)
 
-    def rate(nt, budget):
-        one_pass(nt)
+    def c1_pass(nt):
+        oracle.rms_norm_test_order(x1, wf1, EPS, nthreads=nt)
+
+    def rate(fn, nt, budget):
+        fn(nt)
         n, t0 = 0, time.perf_counter()
         while True:
-            one_pass(nt)
+            fn(nt)
             n += 1
             el = time.perf_counter() - t0
             if el >= budget:
-                return nbytes * n / el / 1e9, n
+                return el / n, n
 
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
-    multi, passes = rate(cores, seconds * 0.7)
-    single, _ = rate(1, seconds * 0.3)
+    cores, visible = cpu_threads()
+    s_multi, passes = rate(chain_pass, cores, seconds * 0.6)
+    s_single, _ = rate(chain_pass, 1, seconds * 0.3)
+    c1_multi, c1_n = rate(c1_pass, cores, seconds * 0.05)
+    c1_single, _ = rate(c1_pass, 1, seconds * 0.05)
     return {
-        "value": round(multi, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-        "sample": f"config-4 chain ops on the first {Ts} tokens ({nbytes} algorithmic bytes per pass), "
-                  f"{passes} passes on {cores} threads; oracle/q3k_oracle.c (C restatement of the reference's "
-                  f"CPU test arithmetic), host {platform.processor() or platform.machine()}",
-        "value_1thread": round(single, 3),
+        "value": round(nbytes / s_multi / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": f"config-4 chain ops (add_rms_norm x2, qk_norm_rope on Q and K with their own weights, silu_mul) "
+                  f"on the first {Ts} tokens ({nbytes} algorithmic bytes per pass), {passes} passes on {cores} "
+                  f"threads; oracle/q3k_oracle.c (C restatement of the reference's CPU arithmetic)",
+        "value_1thread": round(nbytes / s_single / 1e9, 3),
+        "cpu_model": cpu_model(), "cores_visible": visible, "os_cpu_count": os.cpu_count(),
+        "c1": {"what": "config 1: RMSNorm [16, 1024] with the reference test's CPU loop "
+                       "(rms_norm_cuda_test.cpp:174-244)", "bytes": c1_bytes,
+               "us_per_call": round(c1_multi * 1e6, 2), "GB/s": round(c1_bytes / c1_multi / 1e9, 3),
+               "threads": cores, "us_per_call_1thread": round(c1_single * 1e6, 2),
+               "GB/s_1thread": round(c1_bytes / c1_single / 1e9, 3), "calls": c1_n},
     }
 
 
@@ -391,6 +459,105 @@ def weight_io_extra(seconds_limit=180):
     return {"GB/s": r["loader"], "reference_scheme_GB/s": r["reference"], "dma_ceiling_GB/s": r["dma_ceiling"],
             "bytes": r["bytes"], "vs_reference_scheme": round(r["loader"] / r["reference"], 2),
             "frac_of_dma_ceiling": round(r["loader"] / r["dma_ceiling"], 3)}
+
+
+def decode_select_extra(seconds_limit=120):
+    """Per-token selection latency through the C++ runtime (bin/q3k_decode_select_bench, a child process):
+    argmax_last_dimension, Sampler greedy and Sampler with the reference's default sampling over [B, 151936]
+    logits at B = 1 and 64, microseconds per call, and the device allocations made per call once warm."""
+    import subprocess
+
+    exe = os.path.join(REPO, PKG, "bin", "q3k_decode_select_bench")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} is not built"}
+    try:
+        proc = subprocess.run([exe, "--calls", "200"], capture_output=True, text=True, timeout=seconds_limit)
+    except subprocess.TimeoutExpired:
+        return {"error": f"timed out after {seconds_limit} s"}
+    if proc.returncode != 0 or not proc.stdout.strip():
+        return {"error": f"exit {proc.returncode}: {proc.stderr.strip()[-300:]}"}
+    return json.loads(proc.stdout.strip().splitlines()[-1])
+
+
+def c3_decode_extra(q3k, hip, synth, configs, stream):
+    """Config 3 (Qwen3-8B decode step: 64 sequences x 1 token, one position per sequence): the per-layer chain
+    op by op and replayed from a HIP graph (the chain of every input set captured once, one host launch per
+    cycle, as a serving loop replays a decode step).  Each op is a 1-5 MB launch, so this is latency."""
+    c = configs.CONFIGS["c3"]
+    print("[bench] config 3 decode chain", file=sys.stderr, flush=True)
+    base = make_chain_set(hip, synth, configs, c, q3k)
+    sets = [base] + [clone_set(hip, base) for _ in range(5)]
+    make = lambda b: chain_ops(q3k, c, b, stream)  # noqa: E731
+    ms = time_chain(hip, stream, sets, make, 120, 12)
+    out = {"tokens": c.tokens, "chain_bytes": configs.chain_bytes(c), "us_per_layer_op_by_op": round(ms * 1e3, 2)}
+    try:
+        ms_g = time_chain_graph(hip, stream, sets, make, 120, 12)
+        out.update({"us_per_layer_graph_replay": round(ms_g * 1e3, 2),
+                    "tokens_per_s_graph_replay": round(c.tokens / (ms_g * 1e-3), 1),
+                    "GB/s_graph_replay": round(configs.chain_bytes(c) / (ms_g * 1e-3) / 1e9, 1)})
+    except hip.HipRuntimeError as e:
+        out["graph_error"] = str(e)
+    for st in sets:
+        for b in st.values():
+            b.free()
+    return out
+
+
+def c5_extra(q3k, hip, synth, configs, stream, steps):
+    """Config 5 (Qwen3-32B shapes, T = 16384 as 2 x 8192): the fused per-layer chain and each of its ops, plus
+    the final RMSNorm [16384, 5120], in GB/s of algorithmic bytes.  Activations are a 64 MiB block of N(0, 1)
+    bf16 tiled over each buffer by device copies (generating 3.8 GB per input set on the host would take
+    minutes); norm weights N(1, 0.1); the RoPE table of the 8192 positions."""
+    c = configs.CONFIGS["c5"]
+    T, H, I = c.tokens, c.hidden, c.inter
+    print("[bench] config 5 chain", file=sys.stderr, flush=True)
+    block = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, configs.TID_H, (32 << 20,)))
+
+    def act(nbytes):
+        b = hip.DeviceBuffer(nbytes)
+        b.tile_from(block)
+        return b
+
+    DB = hip.DeviceBuffer.from_array
+    weights = {"w1": DB(synth.normal_bf16(c.seed, configs.TID_W1, (H,), mean=1.0, std=0.1)),
+               "w2": DB(synth.normal_bf16(c.seed, configs.TID_W2, (H,), mean=1.0, std=0.1)),
+               "qw": DB(synth.normal_bf16(c.seed, configs.TID_QW, (D,), mean=1.0, std=0.1)),
+               "kw": DB(synth.normal_bf16(c.seed, configs.TID_KW, (D,), mean=1.0, std=0.1)),
+               "cache": DB(q3k.build_rope_cache(c.max_pos, D, configs.THETA))}
+    sets = []
+    for _ in range(2):
+        st = {k: act(T * H * 2) for k in ("h1", "d1", "y1", "h2", "d2", "y2")}
+        st.update({"q": act(T * c.heads_q * D * 2), "k": act(T * c.heads_kv * D * 2),
+                   "g": act(T * I * 2), "u": act(T * I * 2), "o": act(T * I * 2)})
+        st.update(weights)
+        sets.append(st)
+    block.free()
+    make = lambda b: chain_ops(q3k, c, b, stream)  # noqa: E731
+    ms = time_chain(hip, stream, sets, make, max(8, steps // 4), 2)
+    per_op = time_each_op(hip, stream, sets, make, max(8, steps // 4), buffers=OP_BUFFERS)
+    U = c.distinct_positions()
+    op_bytes = {"add_rms_norm_attn": configs.bytes_add_rms_norm(T, H),
+                "qk_norm_rope": configs.bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, D, U),
+                "add_rms_norm_mlp": configs.bytes_add_rms_norm(T, H), "silu_mul": configs.bytes_silu_mul(T, I)}
+    final = time_each_op(hip, stream, sets, lambda b: [
+        ("rms_norm_final", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream))],
+        max(8, steps // 4), buffers={"rms_norm_final": ("h1", "y1")})
+    op_bytes["rms_norm_final"] = configs.bytes_rms_norm(T, H)
+    per_op.update(final)
+    chain = configs.chain_bytes(c)
+    out = {"tokens": T, "chain_bytes": chain, "ms_per_step": round(ms, 5),
+           "GB/s": round(chain / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * chain / (ms * 1e-3) / 1e9 / PEAK_GBS, 2),
+           "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "per_op": {n: {"ms": round(t, 5), "bytes": op_bytes[n], "GB/s": round(op_bytes[n] / (t * 1e-3) / 1e9, 1),
+                          "pct_of_peak": round(100 * op_bytes[n] / (t * 1e-3) / 1e9 / PEAK_GBS, 2)}
+                      for n, t in per_op.items()}}
+    seen = set()
+    for st in sets:
+        for b in st.values():
+            if id(b) not in seen:
+                seen.add(id(b))
+                b.free()
+    return out
 
 
 def main():
@@ -441,11 +608,20 @@ def main():
     dominant = max(per_op, key=per_op.get)
     dom_gbs = op_bytes[dominant] / (per_op[dominant] * 1e-3) / 1e9
     kernel_key = {"silu_mul": "silu_mul", "qk_norm_rope": "qk_norm_rope"}.get(dominant, "add_rms_norm")
+    traffic, traffic_source = read_traffic(kernel_key)
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(dom_gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom_gbs / PEAK_GBS, 4), "traffic": read_traffic(kernel_key),
+                "frac": round(dom_gbs / PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_source,
                 "algorithmic_bytes": op_bytes[dominant]}
 
     extras = {}
+    # final RMSNorm (model.cpp:146) at config 4, timed like the per-op figures: back-to-back launches over
+    # copies of its input and output whose cycle exceeds the Infinity Cache
+    rb = configs.bytes_rms_norm(T, H)
+    ms_rn = time_each_op(hip, stream, sets, lambda b: [
+        ("rms_norm_final", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream))],
+        args.steps, buffers={"rms_norm_final": ("h1", "y1")})["rms_norm_final"]
+    extras["rms_norm_final"] = {"ms": round(ms_rn, 5), "bytes": rb, "GB/s": round(rb / (ms_rn * 1e-3) / 1e9, 1),
+                                "pct_of_peak": round(100 * rb / (ms_rn * 1e-3) / 1e9 / PEAK_GBS, 2)}
     # the same chain replayed from a HIP graph: no host launch cost between ops
     # (what bounds the op-by-op loop at decode sizes)
     try:
@@ -463,13 +639,6 @@ def main():
         extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5),
                                    "per_op_ms": {k: round(v, 5) for k, v in per_unfused.items()},
                                    "fused_speedup": round(ms_unfused / ms_step, 3)}
-        # final RMSNorm (model.cpp:146) at config 4, reading y1 of the rotating sets
-        ms_rn = time_chain(hip, stream, sets, lambda b: [
-            ("rms_norm", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream))],
-            max(10, args.steps), 3)
-        rb = configs.bytes_rms_norm(T, H)
-        extras["rms_norm_final"] = {"ms": round(ms_rn, 5), "bytes": rb,
-                                    "GB/s": round(rb / (ms_rn * 1e-3) / 1e9, 1)}
         # copy ceiling: 1 GiB, 128-bit loads and stores
         nb = 1 << 30
         src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
@@ -565,6 +734,16 @@ def main():
             for e in emb_sets:
                 for buf in e.values():
                     buf.free()
+
+    if not args.no_extras and args.config == "c4":
+        # the other benchmark configs in the same record: their input sets replace config 4's
+        for st in sets:
+            for b in st.values():
+                b.free()
+        extras["c3_decode"] = c3_decode_extra(q3k, hip, synth, configs, stream)
+        extras["c5_prefill"] = c5_extra(q3k, hip, synth, configs, stream, args.steps)
+        print("[bench] decode token selection", file=sys.stderr, flush=True)
+        extras["decode_select"] = decode_select_extra()
 
     if not args.no_extras:
         print("[bench] weight IO", file=sys.stderr, flush=True)

@@ -1,8 +1,12 @@
 /*
- * q3k_bench.h -- measurement aid exported by the same library as q3k_abi.h.
- * It has no counterpart in the reference runtime: it exists so that hardware
- * byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) can be calibrated
- * against a kernel whose traffic is known exactly.
+ * q3k_bench.h -- measurement aids of the benchmark, exported by their own
+ * library (lib/libq3k_bench.so), not by the product library libq3k.so.  No
+ * counterpart in the reference runtime: they exist so that hardware byte
+ * counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) can be calibrated against a
+ * kernel whose traffic is known exactly, and to give the stream ceilings the
+ * kernels are compared with.  Status codes are those of q3k_abi.h; the
+ * message of the last failure on the calling thread comes from
+ * q3k_bench_last_error_string().
  */
 #ifndef Q3K_BENCH_H
 #define Q3K_BENCH_H
@@ -12,6 +16,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Message of the last failing call of this library on the calling thread. */
+Q3K_API const char *q3k_bench_last_error_string(void);
 
 /* dst[0 .. bytes) = src[0 .. bytes) with 128-bit loads and stores; bytes a
  * multiple of 16, both pointers 16-byte aligned, no overlap. */

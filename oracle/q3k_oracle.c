@@ -18,6 +18,7 @@
 #include <float.h>
 #include <math.h>
 #include <pthread.h>
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -88,17 +89,44 @@ static uint16_t bf_of_double(double v) { return BF((float)v); }
 
 typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
 
-struct par_job
-{
-    range_fn fn;
-    void *ctx;
-    int64_t begin, end;
-};
+/* A pool of worker threads kept for the life of the process, grown to the
+ * largest thread count asked for: a call hands part i of [0, n) to worker i
+ * (the caller takes part 0) and returns when every part is done.  Calls are
+ * serialised (one job at a time). */
+#define POOL_MAX 256
+static pthread_mutex_t pool_call = PTHREAD_MUTEX_INITIALIZER;
+static pthread_mutex_t pool_lock = PTHREAD_MUTEX_INITIALIZER;
+static pthread_cond_t pool_go = PTHREAD_COND_INITIALIZER;
+static pthread_cond_t pool_done = PTHREAD_COND_INITIALIZER;
+static int pool_workers = 0;          /* workers started: parts 1 .. pool_workers */
+static unsigned long pool_job = 0;    /* generation of the current job */
+static int pool_parts = 0;            /* parts of the current job */
+static int pool_pending = 0;          /* parts 1 .. pool_parts - 1 not yet finished */
+static range_fn pool_fn;
+static void *pool_ctx;
+static int64_t pool_n;
 
-static void *par_entry(void *arg)
+static void *pool_worker(void *arg)
 {
-    struct par_job *j = (struct par_job *)arg;
-    j->fn(j->ctx, j->begin, j->end);
+    const int part = (int)(intptr_t)arg;
+    unsigned long seen = 0;
+    pthread_mutex_lock(&pool_lock);
+    for (;;)
+    {
+        while (pool_job == seen)
+            pthread_cond_wait(&pool_go, &pool_lock);
+        seen = pool_job;
+        if (part >= pool_parts)
+            continue;
+        const range_fn fn = pool_fn;
+        void *ctx = pool_ctx;
+        const int64_t b = pool_n * part / pool_parts, e = pool_n * (part + 1) / pool_parts;
+        pthread_mutex_unlock(&pool_lock);
+        fn(ctx, b, e);
+        pthread_mutex_lock(&pool_lock);
+        if (--pool_pending == 0)
+            pthread_cond_signal(&pool_done);
+    }
     return NULL;
 }
 
@@ -109,29 +137,35 @@ static void parallel_for(int64_t n, int nthreads, range_fn fn, void *ctx)
         fn(ctx, 0, n);
         return;
     }
-    if (nthreads > 256)
-        nthreads = 256;
+    if (nthreads > POOL_MAX)
+        nthreads = POOL_MAX;
     if ((int64_t)nthreads > n)
         nthreads = (int)n;
-    pthread_t tid[256];
-    struct par_job jobs[256];
-    int started[256];
-    for (int t = 0; t < nthreads; ++t)
+    pthread_mutex_lock(&pool_call);
+    pthread_mutex_lock(&pool_lock);
+    while (pool_workers < nthreads - 1)
     {
-        jobs[t].fn = fn;
-        jobs[t].ctx = ctx;
-        jobs[t].begin = n * t / nthreads;
-        jobs[t].end = n * (t + 1) / nthreads;
-        started[t] = (t > 0) && pthread_create(&tid[t], NULL, par_entry, &jobs[t]) == 0;
+        pthread_t t;
+        if (pthread_create(&t, NULL, pool_worker, (void *)(intptr_t)(pool_workers + 1)) != 0)
+            break;
+        pthread_detach(t);
+        ++pool_workers;
     }
-    fn(ctx, jobs[0].begin, jobs[0].end);
-    for (int t = 1; t < nthreads; ++t)
-    {
-        if (started[t])
-            pthread_join(tid[t], NULL);
-        else
-            fn(ctx, jobs[t].begin, jobs[t].end);
-    }
+    const int parts = pool_workers + 1 < nthreads ? pool_workers + 1 : nthreads;
+    pool_fn = fn;
+    pool_ctx = ctx;
+    pool_n = n;
+    pool_parts = parts;
+    pool_pending = parts - 1;
+    ++pool_job;
+    pthread_cond_broadcast(&pool_go);
+    pthread_mutex_unlock(&pool_lock);
+    fn(ctx, 0, n / parts);
+    pthread_mutex_lock(&pool_lock);
+    while (pool_pending > 0)
+        pthread_cond_wait(&pool_done, &pool_lock);
+    pthread_mutex_unlock(&pool_lock);
+    pthread_mutex_unlock(&pool_call);
 }
 
 /* ---- embedding: src/ops/embedding.cu:29-54 ----------------------------- */
@@ -293,6 +327,43 @@ void q3o_rms_norm(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t N,
 {
     struct rms_ctx c = {NULL, x, NULL, w, N, eps, y, lo, hi};
     parallel_for(rows, nthreads, rms_range, &c);
+}
+
+/* The reference test's CPU loop (tests/unit/rms_norm_cuda_test.cpp:174-244):
+ * the fp32 sum of squares in column order, 1 / sqrt(sum / N + eps), then
+ * the kernel's two roundings. */
+struct rms_seq_ctx
+{
+    const uint16_t *x, *w;
+    int64_t n;
+    float eps;
+    uint16_t *y;
+};
+
+static void rms_seq_range(void *p, int64_t b, int64_t e)
+{
+    const struct rms_seq_ctx *c = (const struct rms_seq_ctx *)p;
+    for (int64_t r = b; r < e; ++r)
+    {
+        const uint16_t *x = c->x + r * c->n;
+        uint16_t *y = c->y + r * c->n;
+        float sum = 0.0f;
+        for (int64_t i = 0; i < c->n; ++i)
+        {
+            const float v = FB(x[i]);
+            sum += v * v;
+        }
+        const float inv = 1.0f / sqrtf(sum / (float)c->n + c->eps);
+        for (int64_t i = 0; i < c->n; ++i)
+            y[i] = BF(FB(BF(FB(x[i]) * inv)) * FB(c->w[i]));
+    }
+}
+
+void q3o_rms_norm_test_order(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t N, float eps, uint16_t *y,
+                             int nthreads)
+{
+    struct rms_seq_ctx c = {x, w, N, eps, y};
+    parallel_for(rows, nthreads, rms_seq_range, &c);
 }
 
 void q3o_add_rms_norm(uint16_t *h, const uint16_t *d, const uint16_t *w, int64_t rows, int64_t N, float eps,

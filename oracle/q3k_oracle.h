@@ -46,6 +46,11 @@ void q3o_add_inplace(uint16_t *d, const uint16_t *s, int64_t n, int nthreads);
 void q3o_rms_norm(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t N, float eps,
                   uint16_t *y, uint16_t *lo, uint16_t *hi, int nthreads);
 
+/* The reference test's own CPU RMSNorm (tests/unit/rms_norm_cuda_test.cpp:
+ * 174-244): fp32 sum of squares in column order; no band. */
+void q3o_rms_norm_test_order(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t N, float eps,
+                             uint16_t *y, int nthreads);
+
 /* add_inplace then rms_norm on the rounded h (decoder_layer.cpp:78->88). h is updated. */
 void q3o_add_rms_norm(uint16_t *h, const uint16_t *d, const uint16_t *w, int64_t rows, int64_t N,
                       float eps, uint16_t *y, uint16_t *lo, uint16_t *hi, int nthreads);

@@ -30,6 +30,7 @@ def lib() -> ctypes.CDLL:
             "q3o_add_inplace": ([_p, _p, _i64, _int], None),
             "q3o_rms_norm": ([_p, _p, _i64, _i64, _f32, _p, _p, _p, _int], None),
             "q3o_add_rms_norm": ([_p, _p, _p, _i64, _i64, _f32, _p, _p, _p, _int], None),
+            "q3o_rms_norm_test_order": ([_p, _p, _i64, _i64, _f32, _p, _int], None),
             "q3o_silu_mul": ([_p, _p, _i64, _p, _p, _p, _int], None),
             "q3o_build_rope_cache": ([_i64, _i32, _f32, _p], _int),
             "q3o_rope": ([_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p, _p, _int], _int),
@@ -98,6 +99,17 @@ def rms_norm(x, w, eps, band=True, nthreads=None):
     lib().q3o_rms_norm(_ptr(x), _ptr(w), x.size // N, N, eps, _ptr(y), _ptr(lo), _ptr(hi),
                        nthreads or default_threads())
     return y, lo, hi
+
+
+def rms_norm_test_order(x, w, eps, nthreads=None):
+    """The reference test's own CPU RMSNorm (rms_norm_cuda_test.cpp:174-244):
+    fp32 sum of squares in column order.  The CPU baseline of config 1."""
+    x = _a(x, np.uint16)
+    w = _a(w, np.uint16)
+    N = w.size
+    y = np.empty_like(x)
+    lib().q3o_rms_norm_test_order(_ptr(x), _ptr(w), x.size // N, N, eps, _ptr(y), nthreads or default_threads())
+    return y
 
 
 def add_rms_norm(h, d, w, eps, band=True, nthreads=None):

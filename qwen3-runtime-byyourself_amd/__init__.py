@@ -23,7 +23,9 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libq3k.so")
 RUNTIME_LIB_PATH = os.path.join(LIB_DIR, "libqwen3_runtime.so")
-ABI_HEADERS = [os.path.join(REPO_DIR, "include", "q3k_abi.h"), os.path.join(REPO_DIR, "include", "q3k_bench.h")]
+BENCH_LIB_PATH = os.path.join(LIB_DIR, "libq3k_bench.so")
+ABI_HEADERS = [os.path.join(REPO_DIR, "include", "q3k_abi.h")]
+BENCH_HEADERS = [os.path.join(REPO_DIR, "include", "q3k_bench.h")]
 
 Q3K_OK = 0
 Q3K_ERR_INVALID_ARGUMENT = 1
@@ -91,17 +93,23 @@ SIGNATURES = {
     "q3k_qk_norm_rope_kv_append_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p,
                                         _p, _p, _i64, _i64, _p],
     "q3k_build_rope_cache_f32": [_p, _i64, _i32, _f32],
-    "q3k_bench_copy_u128": [_p, _p, _i64, _p],
-    "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 
 _lib = None
 
 
-def declared_symbols() -> list[str]:
-    """Function names declared in the public C headers."""
+# name -> argtypes, in the order of include/q3k_bench.h (lib/libq3k_bench.so)
+BENCH_SIGNATURES = {
+    "q3k_bench_copy_u128": [_p, _p, _i64, _p],
+    "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+}
+_bench_lib = None
+
+
+def declared_symbols(headers=None) -> list[str]:
+    """Function names declared in the public C headers (default: the op ABI)."""
     names = []
-    for path in ABI_HEADERS:
+    for path in headers or ABI_HEADERS:
         with open(path) as f:
             text = f.read()
         names += re.findall(r"Q3K_API\s+[\w\s\*]*?\b(q3k_\w+)\s*\(", text)
@@ -129,6 +137,30 @@ def load(path: str | None = None) -> ctypes.CDLL:
     if path is None:
         _lib = lib
     return lib
+
+
+def load_bench() -> ctypes.CDLL:
+    """Load lib/libq3k_bench.so, the benchmark's measurement kernels."""
+    global _bench_lib
+    if _bench_lib is None:
+        load()
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise RuntimeError(f"{BENCH_LIB_PATH} is not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(BENCH_LIB_PATH)
+        for name, argtypes in BENCH_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        lib.q3k_bench_last_error_string.restype = ctypes.c_char_p
+        lib.q3k_bench_last_error_string.argtypes = []
+        _bench_lib = lib
+    return _bench_lib
+
+
+def _check_bench(status: int) -> None:
+    if status != Q3K_OK:
+        msg = load_bench().q3k_bench_last_error_string().decode()
+        raise _ERRORS.get(status, Q3kError)(status, msg)
 
 
 def _check(status: int) -> None:
@@ -251,11 +283,11 @@ def build_rope_cache(P: int, D: int, theta: float):
 
 
 def bench_copy(src, dst, nbytes, stream=None):
-    _check(load().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
+    _check_bench(load_bench().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
 
 
 def bench_read_rows(base, base2, outer, outer_stride, inner, inner_stride, rows, row_stride, row_bytes, sink,
                     stream=None):
     """Read ceiling of a strided row layout (q3k_bench.h); all sizes in bytes."""
-    _check(load().q3k_bench_read_rows_u128(_ptr(base), _ptr(base2), outer, outer_stride, inner, inner_stride, rows,
+    _check_bench(load_bench().q3k_bench_read_rows_u128(_ptr(base), _ptr(base2), outer, outer_stride, inner, inner_stride, rows,
                                            row_stride, row_bytes, _ptr(sink), _ptr(stream)))

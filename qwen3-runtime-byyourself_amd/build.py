@@ -4,6 +4,8 @@ Outputs (in-tree, git-ignored, shipped with the source tree to the GPU box):
 
 * ``lib/libq3k.so``           HIP kernels + the C ABI (``include/q3k_abi.h``),
                                compiled for gfx950 with hipcc.
+* ``lib/libq3k_bench.so``     the benchmark's measurement kernels
+                               (``include/q3k_bench.h``), kept out of libq3k.so.
 * ``lib/libqwen3_runtime.so`` the C++ ``qwen3::`` core tensor layer and the
                                ``qwen3::ops`` drop-in API, linked to libq3k.so.
 * ``tests/cpp/build/*``       C++ test executables (built only when their
@@ -98,6 +100,19 @@ def build_kernels(verbose=False) -> str:
     return out
 
 
+def build_bench_kernels(verbose=False) -> str:
+    """lib/libq3k_bench.so: the benchmark's measurement kernels (include/q3k_bench.h)."""
+    src = os.path.join(BENCH_DIR, "bench_kernels.hip")
+    obj = os.path.join(OBJ_DIR, "bench_kernels.hip.o")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj], verbose=verbose)
+    out = os.path.join(LIB_DIR, "libq3k_bench.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj, *RPATH], verbose=verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build_runtime(verbose=False) -> str | None:
     sources = []
     for d in HOST_DIRS:
@@ -165,7 +180,8 @@ def build_benches(verbose=False) -> list[str]:
 def build_all(verbose=False) -> dict:
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    result = {"kernels": build_kernels(verbose), "oracle": build_oracle(verbose)}
+    result = {"kernels": build_kernels(verbose), "bench_kernels": build_bench_kernels(verbose),
+              "oracle": build_oracle(verbose)}
     result["runtime"] = build_runtime(verbose)
     result["cpp_tests"] = build_cpp_tests(verbose) if result["runtime"] else []
     result["benches"] = build_benches(verbose) if result["runtime"] else []

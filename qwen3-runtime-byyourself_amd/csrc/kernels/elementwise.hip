@@ -26,7 +26,6 @@ namespace q3k
         constexpr bool kRemapAdd = false;
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
-        constexpr int kNtmCopy = 3;
 
         // exp(x) for the SiLU denominator: Cody-Waite style split of
         // x * log2(e) into an integer and a fraction, the fraction through the
@@ -212,55 +211,6 @@ namespace q3k
             return check_launch(name);
         }
 
-        // Plain 128-bit copy used to calibrate hardware byte counters; the same
-        // access pattern as the streaming kernels.
-        __global__ __launch_bounds__(kBlock) void copy_vec_kernel(const Vec8 *src, Vec8 *dst, int64_t nvec)
-        {
-            const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-            if (j < nvec)
-                store8<nt_store(kNtmCopy)>(dst + j, load8<nt_load(kNtmCopy)>(src + j));
-        }
-
-        // Reads the row views of a KV-cache-like layout with 128-bit loads (one
-        // block per view, kReadUnroll row groups in flight per thread) to give
-        // the HBM read ceiling of that access pattern.  Everything read is
-        // XOR-folded into sink, one word per thread, so the loads stay.
-        constexpr int kReadUnroll = 8;
-        __global__ __launch_bounds__(kBlock) void read_rows_kernel(const unsigned char *base,
-                                                                   const unsigned char *base2, int64_t inner,
-                                                                   int64_t outer_stride, int64_t inner_stride,
-                                                                   int64_t rows, int64_t row_stride, int chunks,
-                                                                   uint32_t *sink)
-        {
-            const int64_t view = blockIdx.x;
-            const int64_t off0 = (view / inner) * outer_stride + (view % inner) * inner_stride;
-            const int rows_per_pass = kBlock / chunks;
-            const int r_in = static_cast<int>(threadIdx.x) / chunks, c = static_cast<int>(threadIdx.x) % chunks;
-            const Vec8 zero = {{0u, 0u, 0u, 0u}};
-            uint32_t acc = 0u;
-            for (int64_t r0 = 0; r0 < rows; r0 += static_cast<int64_t>(rows_per_pass) * kReadUnroll)
-            {
-                Vec8 x[kReadUnroll], y[kReadUnroll];
-#pragma unroll
-                for (int u = 0; u < kReadUnroll; ++u)
-                {
-                    const int64_t r = r0 + static_cast<int64_t>(u) * rows_per_pass + r_in;
-                    x[u] = zero;
-                    y[u] = zero;
-                    if (r < rows)
-                    {
-                        const int64_t off = off0 + r * row_stride + 16 * c;
-                        x[u] = load8<false>(reinterpret_cast<const Vec8 *>(base + off));
-                        if (base2 != nullptr)
-                            y[u] = load8<false>(reinterpret_cast<const Vec8 *>(base2 + off));
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < kReadUnroll; ++u)
-                    acc ^= (x[u].d[0] + x[u].d[3]) ^ (y[u].d[1] + y[u].d[2]);
-            }
-            sink[view * kBlock + threadIdx.x] = acc;
-        }
     } // namespace
 } // namespace q3k
 
@@ -291,48 +241,4 @@ extern "C" int q3k_add_inplace_bf16(uint16_t *d, const uint16_t *s, int64_t n, q
     if (!aligned_to(d, 2) || !aligned_to(s, 2))
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "add_inplace pointers must be 2-byte aligned");
     return launch_binary<1>(d, s, d, n, reinterpret_cast<hipStream_t>(stream), "add_inplace");
-}
-
-extern "C" int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3k_stream_t stream)
-{
-    using namespace q3k;
-    if (bytes < 0 || bytes % 16 != 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "copy size must be a non-negative multiple of 16 bytes");
-    if (bytes == 0)
-        return Q3K_OK;
-    if (src == nullptr || dst == nullptr || !aligned16(src) || !aligned16(dst))
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "copy pointers must be non-null and 16-byte aligned");
-    const int64_t nvec = bytes / 16;
-    const int64_t blocks = (nvec + kBlock - 1) / kBlock;
-    if (blocks >= (int64_t{1} << 31))
-        return set_error(Q3K_ERR_OVERFLOW, "copy size exceeds one launch");
-    copy_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        static_cast<const Vec8 *>(src), static_cast<Vec8 *>(dst), nvec);
-    return check_launch("bench_copy_u128");
-}
-
-extern "C" int q3k_bench_read_rows_u128(const void *base, const void *base2, int64_t outer, int64_t outer_stride,
-                                        int64_t inner, int64_t inner_stride, int64_t rows, int64_t row_stride,
-                                        int64_t row_bytes, uint32_t *sink, q3k_stream_t stream)
-{
-    using namespace q3k;
-    if (outer < 0 || inner < 0 || rows < 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "read view counts cannot be negative");
-    if (outer_stride < 0 || inner_stride < 0 || row_stride < 0 || outer_stride % 16 != 0 || inner_stride % 16 != 0 ||
-        row_stride % 16 != 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "read strides must be non-negative multiples of 16 bytes");
-    if (row_bytes < 16 || row_bytes > 16 * kBlock || (row_bytes & (row_bytes - 1)) != 0)
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "read row size must be a power of two from 16 to 4096 bytes");
-    if (outer == 0 || inner == 0 || rows == 0)
-        return Q3K_OK;
-    if (base == nullptr || sink == nullptr || !aligned16(base) || (base2 != nullptr && !aligned16(base2)) ||
-        !aligned_to(sink, 4))
-        return set_error(Q3K_ERR_INVALID_ARGUMENT, "read pointers must be non-null and 16-byte aligned");
-    if (outer > INT32_MAX / inner)
-        return set_error(Q3K_ERR_OVERFLOW, "read view count exceeds one launch");
-    read_rows_kernel<<<dim3(static_cast<unsigned>(outer * inner)), dim3(kBlock), 0,
-                       reinterpret_cast<hipStream_t>(stream)>>>(
-        static_cast<const unsigned char *>(base), static_cast<const unsigned char *>(base2), inner, outer_stride,
-        inner_stride, rows, row_stride, static_cast<int>(row_bytes / 16), sink);
-    return check_launch("bench_read_rows_u128");
 }

@@ -142,12 +142,21 @@ class DeviceBuffer:
             check(runtime().hipMemcpy(out.ctypes.data, self.ptr + offset, out.nbytes, HIP_MEMCPY_D2H), "hipMemcpy D2H")
         return out
 
-    def copy_from(self, other: "DeviceBuffer", nbytes: int | None = None) -> None:
+    def copy_from(self, other: "DeviceBuffer", nbytes: int | None = None, offset: int = 0) -> None:
+        """self[offset : offset + n] = other[0 : n] (n = nbytes, or all of self)."""
         n = self.nbytes if nbytes is None else nbytes
-        if n > self.nbytes or n > other.nbytes:
+        if offset < 0 or offset + n > self.nbytes or n > other.nbytes:
             raise ValueError("device copy exceeds a buffer")
         if n:
-            check(runtime().hipMemcpy(self.ptr, other.ptr, n, HIP_MEMCPY_D2D), "hipMemcpy D2D")
+            check(runtime().hipMemcpy(self.ptr + offset, other.ptr, n, HIP_MEMCPY_D2D), "hipMemcpy D2D")
+
+    def tile_from(self, block: "DeviceBuffer") -> None:
+        """Fills the whole buffer with repeats of ``block`` (device-to-device copies)."""
+        off = 0
+        while off < self.nbytes:
+            n = min(block.nbytes, self.nbytes - off)
+            self.copy_from(block, n, off)
+            off += n
 
     def fill_bytes(self, value: int) -> None:
         if self.nbytes:

@@ -17,10 +17,21 @@ def test_library_exports_every_declared_symbol(q3k):
     assert set(declared) == set(q3k.SIGNATURES) | {"q3k_last_error_string", "q3k_version"}
 
 
+def _exports(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True)
+    return {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+
+
 def test_exports_are_only_the_abi(q3k):
-    out = subprocess.run(["nm", "-D", "--defined-only", q3k.LIB_PATH], capture_output=True, text=True, check=True)
-    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
-    assert exported == set(q3k.declared_symbols())
+    assert _exports(q3k.LIB_PATH) == set(q3k.declared_symbols())
+
+
+def test_bench_library_exports_only_the_measurement_aids(q3k):
+    """The measurement kernels live in lib/libq3k_bench.so, not in the product library."""
+    declared = set(q3k.declared_symbols(q3k.BENCH_HEADERS))
+    assert declared == set(q3k.BENCH_SIGNATURES) | {"q3k_bench_last_error_string"}
+    assert _exports(q3k.BENCH_LIB_PATH) == declared
+    assert not declared & _exports(q3k.LIB_PATH)
 
 
 def test_version(q3k):

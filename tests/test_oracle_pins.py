@@ -172,6 +172,41 @@ def test_rms_norm_dropped_rounding_is_detected(oracle, synth):
         assert_matches_where_unambiguous(y, lo, hi, wrong, "planted")
 
 
+@pytest.mark.parametrize("rows,n", [(16, 1024), (32, 4096), (8, 257)])
+def test_rms_norm_test_order(oracle, synth, rows, n):
+    """The reference test's CPU loop (column-order fp32 sum): within the KAT
+    tolerance of the float64 form, equal to HF torch order where that is
+    unambiguous, and inside the kernel-order oracle's band (only the sum order
+    differs); identical for every thread count."""
+    x = synth.normal_bf16(31, n, (rows, n))
+    w = synth.normal_bf16(31, n + 1, (n,), mean=1.0, std=0.1)
+    y = oracle.rms_norm_test_order(x, w, 1e-6)
+    xf = f32(x).astype(np.float64)
+    expected = xf / np.sqrt((xf**2).mean(axis=1, keepdims=True) + 1e-6) * f32(w)
+    assert np.all(np.abs(f32(y) - expected) <= 0.02 + 0.01 * np.abs(expected))  # rms_norm_cuda_test.cpp:232-235
+    k, lo, hi = oracle.rms_norm(x, w, 1e-6)
+    assert_matches_where_unambiguous(k, lo, hi, y, f"test-order rms_norm[{rows},{n}]")
+    assert_matches_where_unambiguous(k, lo, hi, hf_rms_norm(x, w, 1e-6), f"hf rms_norm[{rows},{n}]")
+    for nt in (1, 3, 8):
+        assert np.array_equal(oracle.rms_norm_test_order(x, w, 1e-6, nthreads=nt), y)
+
+
+def test_rms_norm_test_order_closed_form_and_planted(oracle, synth):
+    n = 1024
+    x = np.full((2, n), 0x3F00, np.uint16)  # 0.5: sum 256 exactly, inv = 1/sqrt(0.25 + 1e-6)
+    w = np.full((n,), 0x3F80, np.uint16)
+    assert np.all(oracle.rms_norm_test_order(x, w, 1e-6) == 0x3F80)
+    # a loop without the RNE(x * inv) rounding would not agree with it everywhere
+    x = synth.normal_bf16(32, 0, (64, n))
+    w = synth.normal_bf16(32, 1, (n,), mean=1.0, std=0.1)
+    y = oracle.rms_norm_test_order(x, w, 1e-6)
+    xf = f32(x)
+    inv = (np.float32(1.0) / np.sqrt(np.cumsum(xf * xf, axis=1, dtype=np.float32)[:, -1:] / np.float32(n)
+                                     + np.float32(1e-6))).astype(np.float32)
+    one_rounding = np_bits(torch.from_numpy((xf * inv * f32(w)).astype(np.float32)).to(torch.bfloat16))
+    assert not np.array_equal(one_rounding, y)
+
+
 def test_rms_norm_constant_row_closed_form(oracle):
     n = 1024
     x = np.full((3, n), 0x3F00, np.uint16)  # 0.5
