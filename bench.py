@@ -34,6 +34,7 @@ import importlib.util
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -332,10 +333,12 @@ def read_traffic(kernel_key):
     with open(path) as f:
         for line in f:
             text = line.strip()
-            if text.startswith("Generated at commit"):
-                source["commit"] = text.split()[-1].strip("`.")
-            elif text.startswith("Kernel sources sha256/16"):
-                source["kernel_sources"] = text.split()[-1].strip("`.")
+            m = re.match(r"Generated at commit `([0-9a-f]+)`", text)
+            if m:
+                source["commit"] = m.group(1)
+            m = re.match(r"Kernel sources sha256/16 `([0-9a-f]+)`", text)
+            if m:
+                source["kernel_sources"] = m.group(1)
             parts = text.strip("|").split("|")
             if len(parts) >= 2 and parts[0].strip() == kernel_key:
                 try:

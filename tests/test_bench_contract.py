@@ -13,3 +13,15 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode != 0
     assert "one GPU only" in proc.stdout + proc.stderr
     assert proc.stdout.strip() == "" or not proc.stdout.lstrip().startswith("{"), "no JSON line for --gpus 2"
+
+
+def test_traffic_provenance_parses_the_committed_profile():
+    """roofline.traffic comes with the profile's file, commit and kernel-source hash, and a stale flag that
+    compares that hash with the kernels in the tree."""
+    import bench
+    value, source = bench.read_traffic("silu_mul")
+    assert isinstance(value, int) and value > 0
+    assert source["file"] == bench.TRAFFIC_PROFILE
+    assert source["commit"] and all(c in "0123456789abcdef" for c in source["commit"])
+    assert len(source["kernel_sources"]) == 16 and len(source["current_kernel_sources"]) == 16
+    assert source["stale"] == (source["kernel_sources"] != source["current_kernel_sources"])
