@@ -102,7 +102,9 @@ Q3K_API int q3k_rms_norm_rows_bf16(const uint16_t *x, const uint16_t *w, uint16_
  * Fused residual add + RMSNorm of selected rows: for i in [0, count), with
  * r = first_row + i * row_stride: h row r = RNE(h row r + d row r) (in place)
  * and y row i = rms_norm(h row r).  Other rows of h are left untouched (after
- * the last layer only the last tokens' residuals are still needed).
+ * the last layer only the last tokens' residuals are still needed).  The
+ * selected rows must be distinct: row_stride 0 with count > 1 is
+ * Q3K_ERR_INVALID_ARGUMENT.
  * Replaces add_inplace at src/model/decoder_layer.cpp:94 of the last layer,
  * rms_norm at src/model/model.cpp:146 and the last-token select of
  * src/model/lm_head.cpp:123-181.

@@ -729,15 +729,18 @@ namespace q3k
         }
 
         template <int G>
-        void launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
+        int launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
         {
             constexpr int QP = kAttWaves * (32 / G);
             a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
+            if (!launch_fits(blocks, kAttBlock) || (a.splits > 1 && !launch_fits(a.rows, kCombineWaves * kWave)))
+                return set_error(Q3K_ERR_OVERFLOW, "GQA grid is too large");
             attn_mfma_kernel<G><<<dim3(static_cast<unsigned>(blocks)), dim3(kAttBlock), 0, stream>>>(a);
             if (a.splits > 1)
                 attn_combine_kernel<<<dim3(static_cast<unsigned>(a.rows)), dim3(kCombineWaves * kWave), 0, stream>>>(
                     a.part_o, a.part_ml, a.out, a.rows, a.splits);
+            return check_launch("grouped_query_attention");
         }
     } // namespace
 } // namespace q3k
@@ -814,17 +817,18 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
         }
         switch (G)
         {
-        case 1: launch_mfma<1>(a, B, s); break;
-        case 2: launch_mfma<2>(a, B, s); break;
-        case 4: launch_mfma<4>(a, B, s); break;
-        case 8: launch_mfma<8>(a, B, s); break;
-        case 16: launch_mfma<16>(a, B, s); break;
-        default: launch_mfma<32>(a, B, s); break;
+        case 1: return launch_mfma<1>(a, B, s);
+        case 2: return launch_mfma<2>(a, B, s);
+        case 4: return launch_mfma<4>(a, B, s);
+        case 8: return launch_mfma<8>(a, B, s);
+        case 16: return launch_mfma<16>(a, B, s);
+        default: return launch_mfma<32>(a, B, s);
         }
-        return check_launch("grouped_query_attention");
     }
     const int64_t rows = B * S * Hq;
-    const int64_t blocks = (rows + (kBlock / kWave) - 1) / (kBlock / kWave);
+    const int64_t blocks = blocks_for(rows, kBlock / kWave);
+    if (!launch_fits(blocks, kBlock))
+        return set_error(Q3K_ERR_OVERFLOW, "GQA grid is too large");
     attn_generic_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(a, rows);
     return check_launch("grouped_query_attention (generic)");
 }

@@ -194,13 +194,11 @@ namespace q3k
             constexpr int NTM = OP == 0 ? kNtmSilu : kNtmAdd;
             constexpr int PR = OP == 0 ? kPrioSilu : 0;
             constexpr bool REMAP = OP == 0 ? kRemapSilu : kRemapAdd;
-            constexpr int64_t kVecPerBlock = static_cast<int64_t>(kBlock) * U;
             const int64_t nvec = n / 8;
-            const int64_t blocks = (nvec + kVecPerBlock - 1) / kVecPerBlock;
-            if (aligned16(a) && aligned16(b) && aligned16(out) && blocks < (int64_t{1} << 31))
+            if (aligned16(a) && aligned16(b) && aligned16(out) && binary_vec_fits(n, U))
             {
-                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, stream>>>(
-                    a, b, out, nvec, n);
+                const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U)));
+                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);
             }
             else
             {

@@ -12,7 +12,7 @@ namespace q3k
 {
     namespace
     {
-        constexpr int kTokensPerBlock = kBlock / kWave;
+        constexpr int kTokensPerBlock = kEmbeddingTokensPerBlock;
         constexpr int kVpt = 8;
         constexpr int kNtm = 2;  // measured: plain loads (random rows), non-temporal stores
 
@@ -90,10 +90,10 @@ extern "C" int q3k_embedding_bf16(const int32_t *ids, int64_t T, const uint16_t 
     if (V > INT64_MAX / H || T > INT64_MAX / H)
         return set_error(Q3K_ERR_OVERFLOW, "embedding size overflows");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t blocks = (T + kTokensPerBlock - 1) / kTokensPerBlock;
-    if (H % 8 == 0 && aligned16(table) && aligned16(out) && blocks < (int64_t{1} << 31))
+    if (H % 8 == 0 && aligned16(table) && aligned16(out) && embedding_vec_fits(T))
     {
-        embedding_vec_kernel<kNtm><<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s>>>(
+        const dim3 grid(static_cast<unsigned>(blocks_for(T, kTokensPerBlock)));
+        embedding_vec_kernel<kNtm><<<grid, dim3(kBlock), 0, s>>>(
             ids, T, reinterpret_cast<const Vec8 *>(table), V, H / 8, reinterpret_cast<Vec8 *>(out));
     }
     else

@@ -6,12 +6,12 @@
 
 #include <stdint.h>
 
+#include "launch_limits.hpp"
 #include "q3k_abi.h"
 #include "q3k_bench.h"
 
 namespace q3k
 {
-    constexpr int kWave = 64;
 
     // Eight bf16 values (16 bytes); element 2i sits in the low half of d[i].
     struct alignas(16) Vec8
@@ -203,7 +203,4 @@ namespace q3k
 
     // Natural alignment of an element pointer (2 for bf16, 4 for int32/float).
     inline bool aligned_to(const void *p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
-
-    // Blocks of 256 threads (four waves) unless stated otherwise.
-    constexpr int kBlock = 256;
 } // namespace q3k

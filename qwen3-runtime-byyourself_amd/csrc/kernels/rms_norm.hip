@@ -326,21 +326,26 @@ namespace q3k
         };
 
         template <int G, int VPT, int MODE>
-        void launch_rows(const Launch &l)
+        bool launch_rows(const Launch &l)
         {
             constexpr int kRowsPerBlock = kBlock / G;
-            const dim3 grid(static_cast<unsigned>((l.rows + kRowsPerBlock - 1) / kRowsPerBlock));
+            if (!rms_rows_fit(l.rows, G))
+                return false;
+            const dim3 grid(static_cast<unsigned>(blocks_for(l.rows, kRowsPerBlock)));
             if (l.nvec == G * VPT)
                 rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), true><<<grid, dim3(kBlock), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
             else
                 rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), false><<<grid, dim3(kBlock), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            return true;
         }
 
         template <int WPR, int VPT, int MODE>
-        void launch_block(const Launch &l)
+        bool launch_block(const Launch &l)
         {
+            if (!rms_block_fits(l.rows, WPR))
+                return false;
             const dim3 grid(static_cast<unsigned>(l.rows)), block(WPR * kWave);
             if (l.nvec == WPR * kWave * VPT)
                 rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, true>
@@ -348,6 +353,7 @@ namespace q3k
             else
                 rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, false>
                     <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            return true;
         }
 
         template <int VPT, int MODE>
@@ -355,14 +361,14 @@ namespace q3k
         {
             switch (waves)
             {
-            case 1: launch_block<1, VPT, MODE>(l); return true;
-            case 2: launch_block<2, VPT, MODE>(l); return true;
-            case 3: launch_block<3, VPT, MODE>(l); return true;
-            case 4: launch_block<4, VPT, MODE>(l); return true;
-            case 5: launch_block<5, VPT, MODE>(l); return true;
-            case 6: launch_block<6, VPT, MODE>(l); return true;
-            case 7: launch_block<7, VPT, MODE>(l); return true;
-            case 8: launch_block<8, VPT, MODE>(l); return true;
+            case 1: return launch_block<1, VPT, MODE>(l);
+            case 2: return launch_block<2, VPT, MODE>(l);
+            case 3: return launch_block<3, VPT, MODE>(l);
+            case 4: return launch_block<4, VPT, MODE>(l);
+            case 5: return launch_block<5, VPT, MODE>(l);
+            case 6: return launch_block<6, VPT, MODE>(l);
+            case 7: return launch_block<7, VPT, MODE>(l);
+            case 8: return launch_block<8, VPT, MODE>(l);
             default: return false;
             }
         }
@@ -381,28 +387,27 @@ namespace q3k
         {
             const int nvec = l.nvec;
             if (nvec <= 1)
-                launch_rows<1, 1, MODE>(l);
+                return launch_rows<1, 1, MODE>(l);
             else if (nvec <= 2)
-                launch_rows<2, 1, MODE>(l);
+                return launch_rows<2, 1, MODE>(l);
             else if (nvec <= 4)
-                launch_rows<4, 1, MODE>(l);
+                return launch_rows<4, 1, MODE>(l);
             else if (nvec <= 8)
-                launch_rows<8, 1, MODE>(l);
+                return launch_rows<8, 1, MODE>(l);
             else if (nvec <= 16)
-                launch_rows<16, 1, MODE>(l);
+                return launch_rows<16, 1, MODE>(l);
             else if (nvec <= 32)
-                launch_rows<32, 1, MODE>(l);
+                return launch_rows<32, 1, MODE>(l);
             else if (nvec <= 64)
-                launch_rows<64, 1, MODE>(l);
+                return launch_rows<64, 1, MODE>(l);
             else if (nvec <= 128)
-                launch_rows<64, 2, MODE>(l);
+                return launch_rows<64, 2, MODE>(l);
             else if (nvec <= 512)
                 return launch_block_waves<1, MODE>((nvec + 63) / 64, l);
             else if (nvec <= 1024)
                 return launch_block_waves<2, MODE>((nvec + 127) / 128, l);
             else
                 return launch_block_waves<4, MODE>((nvec + 255) / 256, l);
-            return true;
         }
 
         constexpr int64_t kMaxFastN = 8 * kWave * 4 * 8; // 16384 elements per row
@@ -414,7 +419,7 @@ namespace q3k
         {
             const bool fast = (n % 8 == 0) && n <= kMaxFastN && aligned16(h) && aligned16(w) && aligned16(y) &&
                               (MODE != kAddNorm || aligned16(d)) && (MODE != kGatherNorm || aligned16(map.table)) &&
-                              rows < (int64_t{1} << 31);
+                              rows < (int64_t{1} << 31);  // each launcher also checks that its grid fits
             const Launch l{h, d, w, y, rows, static_cast<int>(n / 8), 1.0f / static_cast<float>(n), eps, map, stream};
             if (!(fast && launch_fast<MODE>(l)))
             {
@@ -443,10 +448,16 @@ namespace q3k
         }
 
         // Rows first + i * stride, i < count, must lie in [0, INT64_MAX / n).
-        int validate_rows(int64_t count, int64_t first, int64_t stride, int64_t n)
+        // A mode that writes the selected rows back (the residual add) also
+        // needs them distinct: with stride 0 every selected row would be one
+        // row, updated by several rows of the grid at once.
+        int validate_rows(int64_t count, int64_t first, int64_t stride, int64_t n, bool writes_rows)
         {
             if (first < 0 || stride < 0)
                 return set_error(Q3K_ERR_INVALID_ARGUMENT, "RMSNorm row selection cannot be negative");
+            if (writes_rows && stride == 0 && count > 1)
+                return set_error(Q3K_ERR_INVALID_ARGUMENT,
+                                 "add_rms_norm row stride must be positive when more than one row is selected");
             if (count > 0)
             {
                 const int64_t limit = INT64_MAX / n;
@@ -510,7 +521,7 @@ extern "C" int q3k_rms_norm_rows_bf16(const uint16_t *x, const uint16_t *w, uint
     using namespace q3k;
     if (const int st = validate_common(x, w, y, count, N, eps))
         return st;
-    if (const int st = validate_rows(count, first_row, row_stride, N))
+    if (const int st = validate_rows(count, first_row, row_stride, N, false))
         return st;
     if (count == 0)
         return Q3K_OK;
@@ -526,7 +537,7 @@ extern "C" int q3k_add_rms_norm_rows_bf16(uint16_t *h, const uint16_t *d, const 
     using namespace q3k;
     if (const int st = validate_common(h, w, y, count, N, eps))
         return st;
-    if (const int st = validate_rows(count, first_row, row_stride, N))
+    if (const int st = validate_rows(count, first_row, row_stride, N, true))
         return st;
     if (count > 0 && d == nullptr)
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "add_rms_norm delta pointer is null");

@@ -34,8 +34,8 @@ namespace q3k
     {
         constexpr int kHeadDim = 128;
         constexpr int kHalf = kHeadDim / 2;
-        constexpr int kHeadsPerWave = kWave / 16;
-        constexpr int kWavesPerBlock = kBlock / kWave;
+        constexpr int kHeadsPerWave = kRopeHeadsPerWave;
+        constexpr int kWavesPerBlock = kRopeWavesPerBlock;
         constexpr uint32_t kNanPair = 0x7fc07fc0u;
         // NT mode bits (loads | stores) and heads per lane, chosen by measurement.
         constexpr int kNtmRope = 3;
@@ -378,8 +378,7 @@ namespace q3k
             }
         }
 
-        // The fast kernel indexes heads with 32-bit wave-uniform arithmetic.
-        bool grid_ok(int64_t tokens, int32_t heads) { return tokens * heads < (int64_t{1} << 31); }
+        bool grid_ok(int64_t tokens, int32_t heads) { return rope_heads_fit(tokens, heads); }
     } // namespace
 } // namespace q3k
 

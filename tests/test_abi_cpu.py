@@ -131,6 +131,10 @@ def test_caller_fusion_argument_errors(q3k):
     _expect(q3k.rms_norm_rows, ValueError, IA, fake, fake, fake, 4, 0, -8, 1024, 1e-6)
     _expect(q3k.add_rms_norm_rows, OverflowError, OV, fake, fake, fake, fake, 4, 2**61, 1, 1024, 1e-6)
     _expect(q3k.add_rms_norm_rows, ValueError, IA, fake, None, fake, fake, 4, 0, 1, 1024, 1e-6)
+    # the residual add writes its rows back, so they must be distinct rows
+    _expect(q3k.add_rms_norm_rows, ValueError, IA, fake, fake, fake, fake, 2, 0, 0, 1024, 1e-6)
+    _expect(q3k.add_rms_norm_rows, ValueError, IA, fake, fake, fake, fake, 1 << 20, 5, 0, 1024, 1e-6)
+    q3k.add_rms_norm_rows(None, None, None, None, 0, 3, 0, 1024, 1e-6)
     _expect(q3k.embedding_rms_norm, ValueError, IA, fake, 4, fake, 0, 1024, fake, 1e-6, fake, fake)
     _expect(q3k.embedding_rms_norm, ValueError, IA, None, 4, fake, 10, 1024, fake, 1e-6, fake, fake)
     _expect(q3k.embedding_rms_norm, ValueError, IA, fake, 4, fake, 10, 1024, fake, 0.0, fake, fake)
