@@ -4,13 +4,19 @@
 // the same uniform draw: whole rows (counting-sort path) and shuffled top-k
 // candidate lists (the GPU path's input), with heavy ties, signed zeros,
 // top_k at and past the row length, top_p = 1, and draws at 0 and near 1.
+// Also the sampler's argument rules that need no GPU (configuration, logits
+// dtype and device), each with its exception type and message.
 #include "../../qwen3-runtime-byyourself_amd/csrc/generation/row_finish.hpp"
+#include "qwen3/generation/sampler.h"
 #include "test_util.hpp"
 
 #include <algorithm>
 #include <limits>
 #include <random>
 
+using qwen3::generation::Sampler;
+using qwen3::generation::SamplingConfig;
+using qwen3::generation::SamplingMode;
 using qwen3::generation::detail::DrawRule;
 using qwen3::generation::detail::RowFinisher;
 using test::require;
@@ -37,6 +43,58 @@ namespace
         const int32_t cand = f.from_candidates(bits.data(), ids.data(), static_cast<int32_t>(ids.size()), rule, u);
         require(cand == want, what + ": candidates gave " + std::to_string(cand) + ", oracle " + std::to_string(want));
         checked += 2;
+    }
+
+    // The sampler's argument rules that need no GPU, in the order they are
+    // checked: the configuration when a Sampler is made (greedy stops after
+    // the mode), then the logits' dtype and device.
+    template <typename F>
+    void rule(const std::string &row, F &&f, const std::string &message)
+    {
+        bool caught = false;
+        try
+        {
+            f();
+        }
+        catch (const std::invalid_argument &e)
+        {
+            caught = true;
+            require(std::string(e.what()) == message, row + ": message '" + e.what() + "'");
+        }
+        require(caught, row + ": no std::invalid_argument");
+        ++checked;
+    }
+
+    void contract_rows()
+    {
+        const auto make = [](SamplingConfig c) { Sampler s{c}; };
+        const auto with = [](auto edit) {
+            SamplingConfig c;
+            edit(c);
+            return c;
+        };
+        rule("S1 unknown mode", [&] { make(with([](SamplingConfig &c) { c.mode = static_cast<SamplingMode>(7); })); },
+             "unknown sampling mode");
+        for (float t : {0.0F, -1.0F, std::numeric_limits<float>::infinity(), std::numeric_limits<float>::quiet_NaN()})
+            rule("S2 temperature " + std::to_string(t), [&] { make(with([&](SamplingConfig &c) { c.temperature = t; })); },
+                 "sampling temperature must be finite and positive");
+        rule("S3 negative top_k", [&] { make(with([](SamplingConfig &c) { c.top_k = -1; })); },
+             "sampling top_k cannot be negative");
+        for (float p : {0.0F, -0.5F, 1.5F, std::numeric_limits<float>::quiet_NaN()})
+            rule("S4 top_p " + std::to_string(p), [&] { make(with([&](SamplingConfig &c) { c.top_p = p; })); },
+                 "sampling top_p must be in the interval (0, 1]");
+        rule("S order temperature before top_k", [&] {
+            make(with([](SamplingConfig &c) { c.temperature = 0.0F; c.top_k = -1; c.top_p = 2.0F; }));
+        }, "sampling temperature must be finite and positive");
+        // greedy stops after the mode rule: the sampling fields are not read
+        make(with([](SamplingConfig &c) { c.mode = SamplingMode::Greedy; c.temperature = 0.0F; c.top_k = -3; c.top_p = 9.0F; }));
+        Sampler s{SamplingConfig{}};
+        const auto f32 = qwen3::Tensor::empty(qwen3::Shape{2, 8}, qwen3::DType::Float32, qwen3::Device::cpu());
+        const auto cpu = qwen3::Tensor::empty(qwen3::Shape{2, 8}, qwen3::DType::BFloat16, qwen3::Device::cpu());
+        rule("S5 logits dtype", [&] { (void)s.sample(f32); }, "sampler logits must have BFloat16 dtype");
+        rule("S6 logits device", [&] { (void)s.sample(cpu); }, "sampler logits must be on CUDA");
+        auto out = qwen3::Tensor::empty(qwen3::Shape{2, 1}, qwen3::DType::Int32, qwen3::Device::cpu());
+        rule("S6 logits device, sample into", [&] { s.sample(cpu, out); }, "sampler logits must be on CUDA");
     }
 
     void body()
@@ -87,6 +145,7 @@ namespace
         bad[40] = 0x7fc1;   // NaN
         test::require_throws<std::runtime_error>([&] { (void)f.from_row(bad.data(), 64, rules[0], 0.5); }, "NaN accepted");
         std::cout << checked << " rows checked against the oracle\n";
+        contract_rows();
     }
 } // namespace
 
