@@ -90,6 +90,37 @@ namespace
         k2.top_k = 2;
         Sampler sb{k2};
         require_throws<std::runtime_error>([&] { (void)sb.sample(bad); }, "non-finite logit accepted");
+        // logits shape and the valid-vocabulary prefix, checked when sampling
+        const auto message_is = [](const char *row, auto &&f, const std::string &want) {
+            bool caught = false;
+            try
+            {
+                f();
+            }
+            catch (const std::invalid_argument &e)
+            {
+                caught = true;
+                require(std::string(e.what()) == want, std::string(row) + ": message '" + e.what() + "'");
+            }
+            require(caught, std::string(row) + ": accepted");
+        };
+        Sampler plain{SamplingConfig{}};
+        const Tensor rank1 = test::to_gpu(std::vector<uint16_t>(3, 0), Shape{3}, DType::BFloat16);
+        const Tensor no_rows = Tensor::empty(Shape{0, 3}, DType::BFloat16, qwen3::Device::cuda(0));
+        const Tensor no_cols = Tensor::empty(Shape{2, 0}, DType::BFloat16, qwen3::Device::cuda(0));
+        message_is("S7 rank", [&] { (void)plain.sample(rank1); }, "sampler logits must have shape [batch_size, vocab_size]");
+        message_is("S7 batch", [&] { (void)plain.sample(no_rows); }, "sampler batch size must be positive");
+        message_is("S7 vocabulary", [&] { (void)plain.sample(no_cols); }, "sampler vocabulary size must be positive");
+        SamplingConfig neg;
+        neg.valid_vocab_size = -1;
+        Sampler sn{neg};
+        message_is("S8 negative prefix", [&] { (void)sn.sample(logits_of({1.0F, 2.0F, 3.0F}, 1, 3)); },
+                   "valid_vocab_size cannot be negative");
+        SamplingConfig wide;
+        wide.valid_vocab_size = 4;
+        Sampler sw{wide};
+        message_is("S8 prefix past the vocabulary", [&] { (void)sw.sample(logits_of({1.0F, 2.0F, 3.0F}, 1, 3)); },
+                   "valid_vocab_size exceeds logits vocabulary size");
     }
 
     // The GPU top-k path and the whole-row path against the oracle's
