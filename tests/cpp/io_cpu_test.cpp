@@ -9,6 +9,8 @@
 #include "qwen3/io/safetensors_metadata.h"
 #include "test_util.hpp"
 
+#include <cstdlib>
+
 #include <filesystem>
 #include <fstream>
 #include <system_error>
@@ -22,8 +24,12 @@ using test::require_throws;
 
 namespace
 {
+    // tests/golden, found from the executable (tests/cpp/build/<name>) or
+    // named by Q3K_GOLDEN_DIR for a build elsewhere
     fs::path golden_dir()
     {
+        if (const char *d = std::getenv("Q3K_GOLDEN_DIR"))
+            return d;
         return fs::canonical("/proc/self/exe").parent_path().parent_path().parent_path() / "golden";
     }
 
