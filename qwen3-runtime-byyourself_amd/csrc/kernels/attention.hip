@@ -5,7 +5,9 @@
 //
 // Matrix-core path (head_dim 128, unit dim stride, 16-byte rows): a block of
 // four waves owns one (batch, KV head) and QP query positions of all G heads
-// of that group, so every K/V tile it stages in LDS serves G heads.  A wave's
+// of that group, so every K/V tile it stages in LDS serves G heads.  (A
+// decode step with its key range split into short slices runs the same code
+// as one-wave blocks, one slice each.)  A wave's
 // 32 "columns" are (position, head) pairs.  Per 32 keys:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16: A = K rows from LDS,
 //                 B = the wave's Q fragments (registers for the whole loop);
