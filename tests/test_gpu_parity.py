@@ -774,10 +774,14 @@ def test_topk_candidates_ties(q3k, hip, oracle, synth, rows, N, k, levels, split
 
 @pytest.mark.parametrize("B,S,start,Hq,Hkv,cap", [(1, 1, 4095, 32, 8, 4096), (2, 5, 700, 32, 8, 800),
                                                  (1, 1, 300, 64, 8, 320), (1, 3, 400, 16, 8, 420),
-                                                 (4, 1, 1000, 32, 8, 1100)])
+                                                 (4, 1, 1000, 32, 8, 1100), (1, 1, 1000, 8, 8, 1100),
+                                                 (1, 1, 500, 16, 8, 512), (2, 1, 900, 32, 2, 1000),
+                                                 (1, 1, 2000, 32, 1, 2100), (3, 1, 129, 32, 8, 200)])
 def test_gqa_attention_split_keys(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, cap):
     """Decode with few sequences: the key range is split across blocks (the workspace the library asks for) and the
-    slices merged; same band as the single-pass kernel."""
+    slices merged; same band as the single-pass kernel.  Decode steps whose slices hold one or two tiles run as
+    one-wave blocks: covered for every group size G = Hq / Hkv from 1 to 32, and a cache of 130 keys (two slices,
+    the second a partial tile)."""
     D = 128
     name = f"gqa_attention split B={B} S={S} start={start} Hq={Hq} Hkv={Hkv}"
     announce(name)
