@@ -124,10 +124,12 @@ namespace
     }
 
     // The GPU top-k path and the whole-row path against the oracle's
-    // restatement of the reference sampler, over a real vocabulary.
-    void sampler_against_oracle()
+    // restatement of the reference sampler, over a real vocabulary.  From 16
+    // rows on the candidate rows are finished by a row crew (B = 40 here),
+    // with the tie-overflow row among them.
+    void sampler_against_oracle(std::int64_t B)
     {
-        constexpr std::int64_t B = 6, V = 151936, valid = 151669;
+        constexpr std::int64_t V = 151936, valid = 151669;
         std::vector<uint16_t> host(static_cast<std::size_t>(B * V));
         const auto vals = test::values(host.size(), 77, 3.0F);
         host = vals;
@@ -172,7 +174,8 @@ namespace
         const int before = test::current_device();
         argmax_reference_test();
         sampler_reference_test();
-        sampler_against_oracle();
+        sampler_against_oracle(6);
+        sampler_against_oracle(40);
         require(test::current_device() == before, "a sampling call changed the current device");
     }
 } // namespace

@@ -70,8 +70,10 @@ def test_host_runtime_tests_under_sanitizers():
             assert proc.returncode == 0, f"{name} under sanitizers:\n{proc.stdout}\n{proc.stderr[-3000:]}"
 
 
-def test_copy_crew_under_thread_sanitizer():
-    """The staging copy crew (helper threads publishing and finishing copies through atomics) under -fsanitize=thread."""
+@pytest.mark.parametrize("name", ["copy_crew_cpu_test", "row_crew_cpu_test"])
+def test_crews_under_thread_sanitizer(name):
+    """The staging copy crew (helper threads publishing and finishing copies through atomics) and the sampler's row
+    crew (helpers woken per run by a condition variable) under -fsanitize=thread."""
     if shutil.which("g++") is None:
         pytest.skip("g++ not available")
     inc = [f"-I{os.path.join(REPO, 'include')}", f"-I{os.path.join(REPO, 'oracle')}",
@@ -79,11 +81,11 @@ def test_copy_crew_under_thread_sanitizer():
     libs = [os.path.join(REPO, "oracle", "build", "libq3k_oracle.so"),
             "-Wl,-rpath," + os.path.join(REPO, "oracle", "build"), "-pthread"]
     with tempfile.TemporaryDirectory() as tmp:
-        exe = os.path.join(tmp, "copy_crew_tsan")
-        src = os.path.join(REPO, "tests", "cpp", "copy_crew_cpu_test.cpp")
+        exe = os.path.join(tmp, name + "_tsan")
+        src = os.path.join(REPO, "tests", "cpp", name + ".cpp")
         build = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=thread", *inc, src, "-o", exe, *libs],
                                capture_output=True, text=True)
         assert build.returncode == 0, build.stderr[-3000:]
         env = dict(os.environ, TSAN_OPTIONS="halt_on_error=1")
         proc = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
-        assert proc.returncode == 0, f"copy crew under ThreadSanitizer:\n{proc.stdout}\n{proc.stderr[-3000:]}"
+        assert proc.returncode == 0, f"{name} under ThreadSanitizer:\n{proc.stdout}\n{proc.stderr[-3000:]}"
