@@ -168,6 +168,42 @@ namespace
         }
     }
 
+    // A non-finite logit in row 7 of 20 ends the call; the engine then stands
+    // after the draws of rows 0..6, as at the reference's row loop (the draw
+    // comes after the scores, src/generation/sampler.cpp:151,232).  Checked
+    // through the next call's tokens, for the GPU-candidate path and the
+    // whole-row path (both finished by the row crew at 20 rows).
+    void sampler_after_nonfinite_row()
+    {
+        constexpr std::int64_t B = 20, V = 4096;
+        const auto good = test::values(static_cast<std::size_t>(B * V), 91, 2.0F);
+        std::vector<uint16_t> bad = good;
+        bad[static_cast<std::size_t>(7 * V + 123)] = 0x7f80;   // +inf in row 7
+        const Tensor good_t = test::to_gpu(good, Shape{B, V}, DType::BFloat16);
+        const Tensor bad_t = test::to_gpu(bad, Shape{B, V}, DType::BFloat16);
+        for (const std::int32_t top_k : {20, 0})
+        {
+            SamplingConfig cfg;
+            cfg.top_k = top_k;
+            cfg.top_p = 0.9F;
+            cfg.temperature = 0.8F;
+            cfg.seed = 77;
+            Sampler s{cfg};
+            test::require_throws<std::runtime_error>([&] { (void)s.sample(bad_t); }, "non-finite row accepted");
+            const auto got = test::to_host<int32_t>(s.sample(good_t));
+            std::mt19937_64 engine(77);
+            for (int i = 0; i < 7; ++i)
+                (void)engine();
+            for (std::int64_t b = 0; b < B; ++b)
+            {
+                const double u = static_cast<double>(engine() >> 11U) * (1.0 / 9007199254740992.0);
+                const int32_t want = q3o_sample_row(good.data() + b * V, V, cfg.temperature, cfg.top_k, cfg.top_p, u);
+                require(got[static_cast<std::size_t>(b)] == want,
+                        "tokens after a non-finite row: top_k " + std::to_string(top_k));
+            }
+        }
+    }
+
     void body()
     {
         test::require_gpu();
@@ -176,6 +212,7 @@ namespace
         sampler_reference_test();
         sampler_against_oracle(6);
         sampler_against_oracle(40);
+        sampler_after_nonfinite_row();
         require(test::current_device() == before, "a sampling call changed the current device");
     }
 } // namespace
