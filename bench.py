@@ -306,17 +306,29 @@ def time_sampling(q3k, hip, synth, configs, c, stream):
 TRAFFIC_PROFILE = os.path.join("profiles", "pmc_traffic_c4.md")
 
 
-def kernel_source_hash():
-    """sha256 (first 16 hex digits) over the kernel sources, in name order: a rocprof summary records the hash
-    of the sources it measured, so a line can tell whether its traffic figure still describes these kernels."""
+# C++ tokens for the source hash: string and character literals, comments, runs of other non-space
+# characters (a slash alone, so that "a;//c" splits before the comment)
+_CXX_TOKENS = re.compile(r'"(?:\\.|[^"\\\n])*"|\'(?:\\.|[^\'\\\n])*\'|//[^\n]*|/\*.*?\*/|[^\s"\'/]+|/', re.S)
+
+
+def code_tokens(text):
+    """The code of a C++ source without its comments, one space between tokens: edits to comments and layout
+    leave it unchanged."""
+    return " ".join(t for t in _CXX_TOKENS.findall(text) if not t.startswith(("//", "/*")))
+
+
+def kernel_source_hash(kdir=None):
+    """sha256 (first 16 hex digits) over the code of the kernel sources (comments and layout dropped), in name
+    order: a rocprof summary records the hash of the sources it measured, so a line can tell whether its
+    traffic figure still describes these kernels."""
     import hashlib
-    kdir = os.path.join(REPO, PKG, "csrc", "kernels")
+    kdir = kdir or os.path.join(REPO, PKG, "csrc", "kernels")
     h = hashlib.sha256()
     for name in sorted(os.listdir(kdir)):
         if name.endswith((".hip", ".hpp")):
-            h.update(name.encode())
-            with open(os.path.join(kdir, name), "rb") as f:
-                h.update(f.read())
+            h.update(name.encode() + b"\0")
+            with open(os.path.join(kdir, name), encoding="utf-8") as f:
+                h.update(code_tokens(f.read()).encode() + b"\0")
     return h.hexdigest()[:16]
 
 

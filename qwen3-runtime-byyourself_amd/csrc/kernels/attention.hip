@@ -26,12 +26,14 @@
 // from HBM straight into LDS (buffer_load_dwordx4 ... lds, no registers) while
 // the previous tile is computed, into the other of two buffers; one barrier
 // per tile.  The P V product of a tile is issued in the next tile's step,
-// beside that tile's softmax; within one wave the matrix cores and the VALU do
-// not overlap on gfx950 (measured), so the overlap comes from the other
-// block's wave on the same SIMD.  Tile rows are 256 bytes with the 16-byte
-// chunks XOR-swizzled by row so that the K fragment reads (ds_read_b128) and
-// the V transpose reads hit distinct LDS banks.  Prefill grids are renumbered so that the query
-// blocks of one (batch, KV head) run on one XCD and share its L2.
+// beside that tile's softmax.  One wave's independent MFMA and VALU work can
+// overlap on gfx950, but interleaving them within the wave measured slower
+// here than leaving the overlap to the other block's wave on the same SIMD
+// (two waves per SIMD at this register count).  Tile rows are 256 bytes with
+// the 16-byte chunks XOR-swizzled by row so that the K fragment reads
+// (ds_read_b128) and the V transpose reads hit distinct LDS banks.  Prefill
+// grids are renumbered so that the query blocks of one (batch, KV head) run on
+// one XCD and share its L2.
 //
 // Generic path (any head_dim <= 256, any strides): one wave per query row,
 // keys in order, lanes over the head dimension -- the reference's own
