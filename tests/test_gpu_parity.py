@@ -793,3 +793,74 @@ def test_gqa_attention_split_keys(q3k, hip, oracle, synth, B, S, start, Hq, Hkv,
     check_band(oracle, name, got, prim, lo, hi)
     whole = run_attention(q3k, hip, q, store_k, store_v, B, S, Hq, start)
     check_band(oracle, name + " (not split)", whole, prim, lo, hi)
+
+
+def test_prefill_then_decode_matches_one_shot(q3k, hip, oracle, synth):
+    """The reference's end-to-end check of one-shot prefill against prefill + decode
+    (tests/integration/model_real_smoke.cu:101-170), on this library's layer pieces: Q/K norm + RoPE + KV append
+    (self_attention.cpp:147-156) and attention over the cache view.  A prefill of P tokens followed by decode steps
+    of one token each (key-split attention with the workspace the library asks for) leaves the KV cache and the
+    roped queries bit for bit as one prefill of all the tokens does; the prefix rows of attention are bit-identical
+    too (a row's result does not depend on how many positions follow it), and each decode output lies in the
+    oracle's band, as the one-shot rows for the same positions do."""
+    B, P, steps, Hq, Hkv, D = 2, 700, 4, 32, 8, 128
+    T, cap, table_rows = P + steps, P + steps + 20, P + steps + 20
+    name = f"prefill {P} + {steps} decode steps vs one-shot prefill B={B} Hq={Hq} Hkv={Hkv}"
+    announce(name)
+    q = synth.normal_bf16(171, T, (B, T, Hq * D))
+    k = synth.normal_bf16(172, T, (B, T, Hkv * D))
+    v = synth.normal_bf16(173, T, (B, T, Hkv * D))
+    qw = synth.normal_bf16(174, D, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(175, D, (D,), mean=1.0, std=0.1)
+    table = oracle.build_rope_cache(table_rows, D, 1.0e6)
+    QW, KW, C = Guarded(hip, qw), Guarded(hip, kw), Guarded(hip, table)
+    st = (cap * Hkv * D, Hkv * D, D, 1)
+    empty = np.zeros((B, cap, Hkv * D), np.uint16)
+
+    def append(Qb, q_part, k_part, v_part, KC, VC, at):
+        Kb, Vb = Guarded(hip, k_part), Guarded(hip, v_part)
+        q3k.qk_norm_rope_kv_append(Qb, Kb, Vb, QW, KW, B, q_part.shape[1], Hq, Hkv, D, EPS, C, table_rows, at, KC,
+                                   VC, cap, at, None)
+
+    def attend(Qb, KC, VC, S, start, split):
+        O = Guarded(hip, nbytes=B * S * Hq * D * 2)
+        ws = q3k.gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, start + S) if split else 0
+        assert not split or ws > 0, "a decode step over this cache should split the key range"
+        W = Guarded(hip, nbytes=ws) if ws else None
+        q3k.gqa_attention(Qb, KC, VC, O, B, S, Hq, Hkv, D, start + S, start, st, st, workspace=W, workspace_bytes=ws)
+        hip.synchronize()
+        assert O.guards_intact() and (W is None or W.guards_intact())
+        return O.get(np.uint16, (B, S, Hq * D))
+
+    # one prefill of all T tokens
+    Q1, KC1, VC1 = Guarded(hip, q), Guarded(hip, empty), Guarded(hip, empty)
+    append(Q1, q, k, v, KC1, VC1, 0)
+    one_shot = attend(Q1, KC1, VC1, T, 0, False)
+    q1 = Q1.get(np.uint16, q.shape)
+
+    # prefill of P tokens, then one token per step
+    KC2, VC2 = Guarded(hip, empty), Guarded(hip, empty)
+    Qp = Guarded(hip, np.ascontiguousarray(q[:, :P]))
+    append(Qp, q[:, :P], np.ascontiguousarray(k[:, :P]), np.ascontiguousarray(v[:, :P]), KC2, VC2, 0)
+    prefix = attend(Qp, KC2, VC2, P, 0, False)
+    check_exact(name + " prefix queries", Qp.get(np.uint16, (B, P, Hq * D)), q1[:, :P])
+    decoded = []
+    for s in range(P, T):
+        Qd = Guarded(hip, np.ascontiguousarray(q[:, s:s + 1]))
+        append(Qd, q[:, s:s + 1], np.ascontiguousarray(k[:, s:s + 1]), np.ascontiguousarray(v[:, s:s + 1]), KC2,
+               VC2, s)
+        decoded.append(attend(Qd, KC2, VC2, 1, s, True))
+        check_exact(f"{name} step {s} query", Qd.get(np.uint16, (B, 1, Hq * D)), q1[:, s:s + 1])
+    assert all(g.guards_intact() for g in (Q1, KC1, VC1, KC2, VC2, QW, KW, C))
+    check_exact(name + " K cache", KC2.get(np.uint16, empty.shape), KC1.get(np.uint16, empty.shape))
+    check_exact(name + " V cache", VC2.get(np.uint16, empty.shape), VC1.get(np.uint16, empty.shape))
+    check_exact(name + " prefix attention rows", prefix, one_shot[:, :P])
+
+    # the decode rows and the one-shot rows of the same positions, against the oracle on the roped inputs
+    kc = KC1.get(np.uint16, empty.shape)[:, :T].reshape(B, T, Hkv, D)
+    vc = VC1.get(np.uint16, empty.shape)[:, :T].reshape(B, T, Hkv, D)
+    rows = np.array([(b * T + s) * Hq + h for b in range(B) for s in range(P, T) for h in range(Hq)])
+    prim, lo, hi = oracle.gqa_attention(q1, kc, vc, Hq, 0, rows=rows)
+    step_rows = np.stack(decoded, axis=1).reshape(-1, D)   # [B, steps, Hq * D] in (b, s, h) order
+    check_band(oracle, name + " decode rows", step_rows, prim, lo, hi)
+    check_band(oracle, name + " one-shot rows", one_shot.reshape(-1, D)[rows], prim, lo, hi)
