@@ -673,6 +673,17 @@ def main():
         extras["copy_ceiling_GB/s"] = round(2 * nb / (ms_cp * 1e-3) / 1e9, 1)
         src.free()
         dst.free()
+        # the ceiling of SwiGLU's own access pattern at its size: the same two 128-bit input streams and one
+        # output stream with no arithmetic (q3k_bench_stream2_u128), timed like its per-op figure over the same
+        # rotating buffers
+        sb = T * I * 2
+        ms_s2 = time_each_op(hip, stream, sets, lambda b: [
+            ("stream2", lambda: q3k.bench_stream2(b["g"], b["u"], b["o"], sb, stream))],
+            args.steps, buffers={"stream2": OP_BUFFERS["silu_mul"]})["stream2"]
+        s2_gbs = 3 * sb / (ms_s2 * 1e-3) / 1e9
+        extras["silu_mul_pattern_ceiling"] = {
+            "ms": round(ms_s2, 5), "GB/s": round(s2_gbs, 1), "pct_of_peak": round(100 * s2_gbs / PEAK_GBS, 2),
+            "silu_mul_frac": round(ops_report["silu_mul"]["GB/s"] / s2_gbs, 4)}
         # Q/K norm + RoPE + KV-cache append (self_attention.cpp:147-156) fused, against qk_norm_rope followed by
         # the append; the cache holds the whole sequence (capacity S), written at cached length 0
         print("[bench] timing KV append", file=sys.stderr, flush=True)

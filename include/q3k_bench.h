@@ -24,6 +24,11 @@ Q3K_API const char *q3k_bench_last_error_string(void);
  * multiple of 16, both pointers 16-byte aligned, no overlap. */
 Q3K_API int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3k_stream_t stream);
 
+/* dst[i] = a[i] XOR b[i] over `bytes` bytes with 128-bit loads and stores:
+ * the access pattern of the two-input streaming ops (silu_mul, add) with no
+ * arithmetic.  bytes a multiple of 16, pointers 16-byte aligned. */
+Q3K_API int q3k_bench_stream2_u128(const void *a, const void *b, void *dst, int64_t bytes, q3k_stream_t stream);
+
 /* Read ceiling of a strided row layout such as a KV-cache view: outer x inner
  * views, view (o, i) at base + o * outer_stride + i * inner_stride, each
  * `rows` rows of row_bytes at row_stride (bytes; strides multiples of 16,

@@ -101,6 +101,7 @@ _lib = None
 # name -> argtypes, in the order of include/q3k_bench.h (lib/libq3k_bench.so)
 BENCH_SIGNATURES = {
     "q3k_bench_copy_u128": [_p, _p, _i64, _p],
+    "q3k_bench_stream2_u128": [_p, _p, _p, _i64, _p],
     "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 _bench_lib = None
@@ -284,6 +285,11 @@ def build_rope_cache(P: int, D: int, theta: float):
 
 def bench_copy(src, dst, nbytes, stream=None):
     _check_bench(load_bench().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
+
+
+def bench_stream2(a, b, dst, nbytes, stream=None):
+    """dst = a XOR b with the two-input ops' 128-bit loads and stores (q3k_bench.h)."""
+    _check_bench(load_bench().q3k_bench_stream2_u128(_ptr(a), _ptr(b), _ptr(dst), nbytes, _ptr(stream)))
 
 
 def bench_read_rows(base, base2, outer, outer_stride, inner, inner_stride, rows, row_stride, row_bytes, sink,

@@ -602,6 +602,21 @@ def test_bench_read_rows(q3k, hip):
     check_exact("bench_read_rows sink", got, want)
 
 
+def test_bench_stream2(q3k, hip):
+    """The two-stream ceiling aid reads both inputs and writes exactly its output: dst = a XOR b, word for word,
+    over a size that leaves a partial last block, and nothing outside dst."""
+    announce("bench_stream2")
+    n = 16 * 1000 + 16 * 37          # bytes: 1037 vectors
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
+    b = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
+    A, B, O = Guarded(hip, a), Guarded(hip, b), Guarded(hip, nbytes=n)
+    q3k.bench_stream2(A, B, O, n)
+    hip.synchronize()
+    assert A.guards_intact() and B.guards_intact() and O.guards_intact()
+    check_exact("bench_stream2", O.get(np.uint32, (n // 4,)), a ^ b)
+
+
 @pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
 def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
     """Benchmark-size prefill (config 4 shape, and a 4096-token sequence): every row computed on the GPU, a seeded
