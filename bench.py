@@ -207,6 +207,27 @@ def op_rotation(hip, sets, keys):
     return out
 
 
+def pattern_ceiling(hip, q3k, stream, nbytes, n_in, n_out, in_place, reps):
+    """GB/s of the stream aid (q3k_bench_stream_u128) with n_in input and n_out output streams of nbytes each,
+    the first output written over the first input when in_place, back to back over enough buffer sets that one
+    cycle exceeds MIN_CYCLE_BYTES (contents are whatever the allocations hold: nothing depends on them)."""
+    n_bufs = n_in + n_out - (1 if in_place else 0)
+    count = max(2, -(-MIN_CYCLE_BYTES // (nbytes * n_bufs)))
+    rot = []
+    for _ in range(count):
+        bufs = [hip.DeviceBuffer(nbytes) for _ in range(n_bufs)]
+        ins = bufs[:n_in] + [None] * (2 - n_in)
+        outs = ([bufs[0]] if in_place else []) + bufs[n_in:]
+        outs = outs + [None] * (2 - len(outs))
+        rot.append((ins[0], ins[1], outs[0], outs[1]))
+    ms = time_chain(hip, stream, rot, lambda r: [("stream", lambda: q3k.bench_stream(*r, nbytes, stream))],
+                    max(reps, len(rot)), 2)
+    for r in rot:
+        for buf in {id(x): x for x in r if x is not None}.values():
+            buf.free()
+    return (n_in + n_out) * nbytes / (ms * 1e-3) / 1e9
+
+
 def time_each_op(hip, stream, sets, make_ops, reps, warmup=2, buffers=None):
     """Per-op duration: `reps` back-to-back launches of one op, rotating over
     input sets whose cycle exceeds the Infinity Cache (so every launch reads
@@ -673,17 +694,19 @@ def main():
         extras["copy_ceiling_GB/s"] = round(2 * nb / (ms_cp * 1e-3) / 1e9, 1)
         src.free()
         dst.free()
-        # the ceiling of SwiGLU's own access pattern at its size: the same two 128-bit input streams and one
-        # output stream with no arithmetic (q3k_bench_stream2_u128), timed like its per-op figure over the same
-        # rotating buffers
-        sb = T * I * 2
-        ms_s2 = time_each_op(hip, stream, sets, lambda b: [
-            ("stream2", lambda: q3k.bench_stream2(b["g"], b["u"], b["o"], sb, stream))],
-            args.steps, buffers={"stream2": OP_BUFFERS["silu_mul"]})["stream2"]
-        s2_gbs = 3 * sb / (ms_s2 * 1e-3) / 1e9
-        extras["silu_mul_pattern_ceiling"] = {
-            "ms": round(ms_s2, 5), "GB/s": round(s2_gbs, 1), "pct_of_peak": round(100 * s2_gbs / PEAK_GBS, 2),
-            "silu_mul_frac": round(ops_report["silu_mul"]["GB/s"] / s2_gbs, 4)}
+        # each fused op's own access-pattern ceiling at its size: the same 128-bit input and output streams with
+        # no arithmetic (q3k_bench_stream_u128), back to back over rotating buffers like the per-op figures
+        print("[bench] timing access-pattern ceilings", file=sys.stderr, flush=True)
+        q_bytes = T * (c.heads_q + c.heads_kv) * D * 2
+        patterns = {"silu_mul": (T * I * 2, 2, 1, False), "add_rms_norm_attn": (T * H * 2, 2, 2, True),
+                    "qk_norm_rope": (q_bytes, 1, 1, True)}
+        ceilings = {}
+        for name, (nb_op, n_in, n_out, in_place) in patterns.items():
+            gbs = pattern_ceiling(hip, q3k, stream, nb_op, n_in, n_out, in_place, args.steps)
+            ceilings[name] = {"streams": f"{n_in} in, {n_out} out" + (" (first in place)" if in_place else ""),
+                              "bytes_each": nb_op, "GB/s": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+                              "op_frac": round(ops_report[name]["GB/s"] / gbs, 4)}
+        extras["pattern_ceilings"] = ceilings
         # Q/K norm + RoPE + KV-cache append (self_attention.cpp:147-156) fused, against qk_norm_rope followed by
         # the append; the cache holds the whole sequence (capacity S), written at cached length 0
         print("[bench] timing KV append", file=sys.stderr, flush=True)

@@ -24,10 +24,14 @@ Q3K_API const char *q3k_bench_last_error_string(void);
  * multiple of 16, both pointers 16-byte aligned, no overlap. */
 Q3K_API int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3k_stream_t stream);
 
-/* dst[i] = a[i] XOR b[i] over `bytes` bytes with 128-bit loads and stores:
- * the access pattern of the two-input streaming ops (silu_mul, add) with no
- * arithmetic.  bytes a multiple of 16, pointers 16-byte aligned. */
-Q3K_API int q3k_bench_stream2_u128(const void *a, const void *b, void *dst, int64_t bytes, q3k_stream_t stream);
+/* One or two streams in, one or two out, over `bytes` bytes each, with
+ * 128-bit loads and stores and no arithmetic to speak of: out0 = in0 XOR in1,
+ * out1 = in0 + in1 word by word (in1 and out1 nullable; a missing in1 reads
+ * as zero).  out0 may be in0 (in place).  The access pattern of a streaming op
+ * at its size: silu_mul is (g, u) -> out, add + RMSNorm (h, d) -> (h, y), the
+ * in-place RoPE q -> q.  bytes a multiple of 16, pointers 16-byte aligned. */
+Q3K_API int q3k_bench_stream_u128(const void *in0, const void *in1, void *out0, void *out1, int64_t bytes,
+                                  q3k_stream_t stream);
 
 /* Read ceiling of a strided row layout such as a KV-cache view: outer x inner
  * views, view (o, i) at base + o * outer_stride + i * inner_stride, each

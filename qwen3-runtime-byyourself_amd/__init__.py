@@ -101,7 +101,7 @@ _lib = None
 # name -> argtypes, in the order of include/q3k_bench.h (lib/libq3k_bench.so)
 BENCH_SIGNATURES = {
     "q3k_bench_copy_u128": [_p, _p, _i64, _p],
-    "q3k_bench_stream2_u128": [_p, _p, _p, _i64, _p],
+    "q3k_bench_stream_u128": [_p, _p, _p, _p, _i64, _p],
     "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 _bench_lib = None
@@ -287,9 +287,10 @@ def bench_copy(src, dst, nbytes, stream=None):
     _check_bench(load_bench().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
 
 
-def bench_stream2(a, b, dst, nbytes, stream=None):
-    """dst = a XOR b with the two-input ops' 128-bit loads and stores (q3k_bench.h)."""
-    _check_bench(load_bench().q3k_bench_stream2_u128(_ptr(a), _ptr(b), _ptr(dst), nbytes, _ptr(stream)))
+def bench_stream(in0, in1, out0, out1, nbytes, stream=None):
+    """out0 = in0 XOR in1, out1 = in0 + in1 (in1, out1 may be None) with 128-bit loads and stores (q3k_bench.h)."""
+    _check_bench(load_bench().q3k_bench_stream_u128(_ptr(in0), _ptr(in1), _ptr(out0), _ptr(out1), nbytes,
+                                                    _ptr(stream)))
 
 
 def bench_read_rows(base, base2, outer, outer_stride, inner, inner_stride, rows, row_stride, row_bytes, sink,

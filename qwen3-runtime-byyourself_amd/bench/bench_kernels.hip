@@ -3,8 +3,8 @@
 // the kernels of the op API.  Not part of the runtime: a plain 128-bit copy
 // whose bytes are known exactly (to calibrate rocprofv3 FETCH_SIZE /
 // WRITE_SIZE and to give the stream ceiling of a launch size), the same with
-// two input streams (the two-input ops' pattern), and a reader of a strided
-// row layout (the HBM read ceiling of a KV-cache view).
+// one or two streams in and out (an op's own pattern), and a reader of a
+// strided row layout (the HBM read ceiling of a KV-cache view).
 #include "../csrc/kernels/q3k_common.hpp"
 
 #include <cstdarg>
@@ -41,22 +41,29 @@ namespace q3k
                 store8<nt_store(kNtmCopy)>(dst + j, load8<nt_load(kNtmCopy)>(src + j));
         }
 
-        // Two 128-bit streams in, one out (dst = a XOR b), with the loads and
-        // stores of the two-input streaming ops (SwiGLU, residual add): the
-        // HBM ceiling of that access pattern at a given size.
-        __global__ __launch_bounds__(kBlock) void stream2_vec_kernel(const Vec8 *a, const Vec8 *b, Vec8 *dst,
-                                                                     int64_t nvec)
+        // One or two 128-bit streams in, one or two out, with the loads and
+        // stores of the streaming ops: out0 = in0 XOR in1, out1 = in0 + in1
+        // (word-wise; in1 absent reads as zero).  In place when out0 is in0.
+        // The HBM ceiling of an op's access pattern at its size.
+        __global__ __launch_bounds__(kBlock) void stream_vec_kernel(const Vec8 *in0, const Vec8 *in1, Vec8 *out0,
+                                                                    Vec8 *out1, int64_t nvec)
         {
             const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-            if (j < nvec)
-            {
-                const Vec8 x = load8<nt_load(kNtmCopy)>(a + j), y = load8<nt_load(kNtmCopy)>(b + j);
-                Vec8 r;
+            if (j >= nvec)
+                return;
+            const Vec8 zero = {{0u, 0u, 0u, 0u}};
+            const Vec8 x = load8<nt_load(kNtmCopy)>(in0 + j);
+            const Vec8 y = in1 != nullptr ? load8<nt_load(kNtmCopy)>(in1 + j) : zero;
+            Vec8 r, t;
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    r.d[k] = x.d[k] ^ y.d[k];
-                store8<nt_store(kNtmCopy)>(dst + j, r);
+            for (int k = 0; k < 4; ++k)
+            {
+                r.d[k] = x.d[k] ^ y.d[k];
+                t.d[k] = x.d[k] + y.d[k];
             }
+            store8<nt_store(kNtmCopy)>(out0 + j, r);
+            if (out1 != nullptr)
+                store8<nt_store(kNtmCopy)>(out1 + j, t);
         }
 
         // Reads the row views of a KV-cache-like layout with 128-bit loads (one
@@ -122,22 +129,25 @@ extern "C" int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3
     return bench_launch_status("bench_copy_u128");
 }
 
-extern "C" int q3k_bench_stream2_u128(const void *a, const void *b, void *dst, int64_t bytes, q3k_stream_t stream)
+extern "C" int q3k_bench_stream_u128(const void *in0, const void *in1, void *out0, void *out1, int64_t bytes,
+                                     q3k_stream_t stream)
 {
     using namespace q3k;
     if (bytes < 0 || bytes % 16 != 0)
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream size must be a non-negative multiple of 16 bytes");
     if (bytes == 0)
         return Q3K_OK;
-    if (a == nullptr || b == nullptr || dst == nullptr || !aligned16(a) || !aligned16(b) || !aligned16(dst))
-        return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream pointers must be non-null and 16-byte aligned");
+    if (in0 == nullptr || out0 == nullptr || !aligned16(in0) || !aligned16(out0) ||
+        (in1 != nullptr && !aligned16(in1)) || (out1 != nullptr && !aligned16(out1)))
+        return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream pointers must be 16-byte aligned (in0, out0 non-null)");
     const int64_t nvec = bytes / 16;
     const int64_t blocks = (nvec + kBlock - 1) / kBlock;
     if (blocks >= (int64_t{1} << 31))
         return bench_error(Q3K_ERR_OVERFLOW, "stream size exceeds one launch");
-    stream2_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        static_cast<const Vec8 *>(a), static_cast<const Vec8 *>(b), static_cast<Vec8 *>(dst), nvec);
-    return bench_launch_status("bench_stream2_u128");
+    stream_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        static_cast<const Vec8 *>(in0), static_cast<const Vec8 *>(in1), static_cast<Vec8 *>(out0),
+        static_cast<Vec8 *>(out1), nvec);
+    return bench_launch_status("bench_stream_u128");
 }
 
 extern "C" int q3k_bench_read_rows_u128(const void *base, const void *base2, int64_t outer, int64_t outer_stride,

@@ -602,19 +602,28 @@ def test_bench_read_rows(q3k, hip):
     check_exact("bench_read_rows sink", got, want)
 
 
-def test_bench_stream2(q3k, hip):
-    """The two-stream ceiling aid reads both inputs and writes exactly its output: dst = a XOR b, word for word,
-    over a size that leaves a partial last block, and nothing outside dst."""
-    announce("bench_stream2")
+@pytest.mark.parametrize("n_in,n_out,in_place", [(2, 1, False), (2, 2, True), (1, 1, True), (1, 2, False)])
+def test_bench_stream(q3k, hip, n_in, n_out, in_place):
+    """The access-pattern ceiling aid reads its inputs and writes exactly its outputs: out0 = in0 XOR in1,
+    out1 = in0 + in1 word for word (a missing in1 reads as zero), in place over in0 when asked, over a size that
+    leaves a partial last block, and nothing outside the buffers."""
+    announce(f"bench_stream in={n_in} out={n_out} in_place={in_place}")
     n = 16 * 1000 + 16 * 37          # bytes: 1037 vectors
     rng = np.random.default_rng(11)
     a = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
-    b = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
-    A, B, O = Guarded(hip, a), Guarded(hip, b), Guarded(hip, nbytes=n)
-    q3k.bench_stream2(A, B, O, n)
+    b = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32) if n_in == 2 else np.zeros(n // 4, np.uint32)
+    A = Guarded(hip, a)
+    B = Guarded(hip, b) if n_in == 2 else None
+    O0 = A if in_place else Guarded(hip, nbytes=n)
+    O1 = Guarded(hip, nbytes=n) if n_out == 2 else None
+    q3k.bench_stream(A, B, O0, O1, n)
     hip.synchronize()
-    assert A.guards_intact() and B.guards_intact() and O.guards_intact()
-    check_exact("bench_stream2", O.get(np.uint32, (n // 4,)), a ^ b)
+    assert all(g.guards_intact() for g in (A, B, O0, O1) if g is not None)
+    check_exact("bench_stream out0", O0.get(np.uint32, (n // 4,)), a ^ b)
+    if O1 is not None:
+        check_exact("bench_stream out1", O1.get(np.uint32, (n // 4,)), (a + b).astype(np.uint32))
+    if B is not None:
+        check_exact("bench_stream in1 unchanged", B.get(np.uint32, (n // 4,)), b)
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
