@@ -626,10 +626,11 @@ def test_bench_stream(q3k, hip, n_in, n_out, in_place):
         check_exact("bench_stream in1 unchanged", B.get(np.uint32, (n // 4,)), b)
 
 
-@pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128)])
+@pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128), (1, 8192, 64, 8, 192)])
 def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
-    """Benchmark-size prefill (config 4 shape, and a 4096-token sequence): every row computed on the GPU, a seeded
-    sample of rows (always including the last positions, the longest contexts) checked against the oracle."""
+    """Benchmark-size prefill (config 4 shape, a 4096-token sequence, and one 8192-token sequence of the config-5
+    model's 64 query heads over 8 KV heads): every row computed on the GPU, a seeded sample of rows (always
+    including the last positions, the longest contexts) checked against the oracle."""
     D = 128
     name = f"gqa_attention prefill B={B} S={S} Hq={Hq} Hkv={Hkv} rows={nrows}"
     announce(name)
