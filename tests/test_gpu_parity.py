@@ -271,6 +271,59 @@ def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, o
     check_band(oracle, name + " k", gk, pk, lk, hk)
 
 
+def _special_rows(synth, rows, n, seed):
+    """Rows of normal values with one special case each: +inf, -inf, NaN, values whose squares overflow fp32,
+    all zeros, values near the smallest normal, and a row spanning +-3e38; the rest stay normal."""
+    f = synth.bf16_to_f32(synth.normal_bf16(seed, n, (rows, n))).copy()
+    special = [lambda r: r.__setitem__(3, np.inf), lambda r: r.__setitem__(n // 2, -np.inf),
+               lambda r: r.__setitem__(n - 1, np.nan), lambda r: r.__setitem__(slice(None), r * 2.0e37),
+               lambda r: r.__setitem__(slice(None), 0.0), lambda r: r.__setitem__(slice(None), r * 1.5e-38),
+               lambda r: r.__setitem__(slice(0, 2), [3.0e38, -3.0e38])]
+    for i, fn in enumerate(special[:rows]):
+        fn(f[i])
+    return synth.f32_to_bf16(f.astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [4096, 128])
+def test_norms_special_values(q3k, hip, oracle, synth, n):
+    """RMSNorm and add + RMSNorm on rows holding +-inf, NaN, overflowing squares, zeros and near-underflow
+    values (the reference's arithmetic propagates them: an infinite sum of squares gives 1/rms = 0, so finite
+    elements become 0 and infinite ones NaN): the same non-finite pattern and the same finite values, within the
+    band, as the oracle."""
+    rows = 9
+    name = f"norm special values N={n}"
+    announce(name)
+    x = _special_rows(synth, rows, n, 120)
+    w = synth.normal_bf16(121, n, (n,), mean=1.0, std=0.1)
+    prim, lo, hi = oracle.rms_norm(x, w, EPS)
+    check_band(oracle, name, run_rms(q3k, hip, x, w), prim, lo, hi)
+    d = _special_rows(synth, rows, n, 122)[::-1].copy()
+    h_out, y = run_add_rms(q3k, hip, x, d, w)
+    h_ref, prim, lo, hi = oracle.add_rms_norm(x, d, w, EPS)
+    # the residual is bit-exact except that NaN payloads may differ
+    nan_got, nan_ref = np.isnan(synth.bf16_to_f32(h_out)), np.isnan(synth.bf16_to_f32(h_ref))
+    assert np.array_equal(nan_got, nan_ref), "residual NaN positions differ"
+    check_exact(name + " add residual", h_out[~nan_ref], h_ref[~nan_ref])
+    check_band(oracle, name + " add", y, prim, lo, hi)
+
+
+def test_qk_norm_rope_special_values(q3k, hip, oracle, synth):
+    """Q/K norm + RoPE on heads holding +-inf, NaN, overflowing squares, zeros and near-underflow values: the
+    norm's zero or NaN results pass through the rotation as in the oracle."""
+    B, S, Hq, Hkv, D = 1, 3, 4, 4, 128
+    announce("qk_norm_rope special values")
+    cache = q3k.build_rope_cache(S + 1, D, 1.0e6)
+    q = _special_rows(synth, B * S * Hq, D, 123).reshape(B, S, Hq * D)
+    k = _special_rows(synth, B * S * Hkv, D, 124)[::-1].copy().reshape(B, S, Hkv * D)
+    qw = synth.normal_bf16(125, D, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(126, D, (D,), mean=1.0, std=0.1)
+    gq, gk = run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache)
+    pq, lq, hq = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, cache)
+    pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache)
+    check_band(oracle, "qk special q", gq, pq, lq, hq)
+    check_band(oracle, "qk special k", gk, pk, lk, hk)
+
+
 def test_qk_norm_rope_positions_overload(q3k, hip, oracle, synth):
     announce("qk_norm_rope positions")
     B, S, Hq, Hkv, D, P = 64, 1, 32, 8, 128, 4096
