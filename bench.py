@@ -264,7 +264,8 @@ def time_attention(q3k, hip, synth, c, stream):
         ws = hip.DeviceBuffer(wb) if wb else None   # a launch too small for the GPU splits the key range
         ms = time_chain(hip, stream, [0], lambda _: [
             ("attention", lambda: q3k.gqa_attention(q, kc, vc, o, B, S, c.heads_q, c.heads_kv, D, L, start, st, st,
-                                                    stream, workspace=ws, workspace_bytes=wb))], 10 if S > 1 else 50, 2)
+                                                    stream, workspace=ws, workspace_bytes=wb))],
+                        50, 50 if S > 1 else 5)
         flops = attention_flops(B, S, start, c.heads_q, D)
         byts = 2 * B * L * c.heads_kv * D * 2 + 2 * B * S * c.heads_q * D * 2
         rec = {"ms": round(ms, 5), "B": B, "S": S, "cached": L, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
