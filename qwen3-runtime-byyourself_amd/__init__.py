@@ -283,18 +283,36 @@ def build_rope_cache(P: int, D: int, theta: float):
     return out
 
 
+def _need(buf, nbytes, what):
+    """The C ABI takes bare addresses; a buffer object that knows its size is
+    checked against the bytes the call will touch before anything launches."""
+    have = getattr(buf, "nbytes", None)
+    if buf is not None and have is not None and have < nbytes:
+        raise ValueError(f"{what} holds {have} bytes, the call touches {nbytes}")
+
+
 def bench_copy(src, dst, nbytes, stream=None):
+    _need(src, nbytes, "bench_copy source")
+    _need(dst, nbytes, "bench_copy destination")
     _check_bench(load_bench().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
 
 
 def bench_stream(in0, in1, out0, out1, nbytes, stream=None):
     """out0 = in0 XOR in1, out1 = in0 + in1 (in1, out1 may be None) with 128-bit loads and stores (q3k_bench.h)."""
+    for buf, what in ((in0, "in0"), (in1, "in1"), (out0, "out0"), (out1, "out1")):
+        _need(buf, nbytes, "bench_stream " + what)
     _check_bench(load_bench().q3k_bench_stream_u128(_ptr(in0), _ptr(in1), _ptr(out0), _ptr(out1), nbytes,
                                                     _ptr(stream)))
 
 
 def bench_read_rows(base, base2, outer, outer_stride, inner, inner_stride, rows, row_stride, row_bytes, sink,
                     stream=None):
-    """Read ceiling of a strided row layout (q3k_bench.h); all sizes in bytes."""
+    """Read ceiling of a strided row layout (q3k_bench.h); all sizes in bytes.  The kernel writes one 4-byte
+    word per thread to sink: outer * inner * 256 words."""
+    if outer > 0 and inner > 0 and rows > 0:
+        last = (outer - 1) * outer_stride + (inner - 1) * inner_stride + (rows - 1) * row_stride + row_bytes
+        _need(base, last, "bench_read_rows base")
+        _need(base2, last, "bench_read_rows base2")
+        _need(sink, outer * inner * 256 * 4, "bench_read_rows sink")
     _check_bench(load_bench().q3k_bench_read_rows_u128(_ptr(base), _ptr(base2), outer, outer_stride, inner, inner_stride, rows,
                                            row_stride, row_bytes, _ptr(sink), _ptr(stream)))

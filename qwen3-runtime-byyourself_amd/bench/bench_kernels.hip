@@ -122,7 +122,7 @@ extern "C" int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "copy pointers must be non-null and 16-byte aligned");
     const int64_t nvec = bytes / 16;
     const int64_t blocks = (nvec + kBlock - 1) / kBlock;
-    if (blocks >= (int64_t{1} << 31))
+    if (!launch_fits(blocks, kBlock))
         return bench_error(Q3K_ERR_OVERFLOW, "copy size exceeds one launch");
     copy_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
         static_cast<const Vec8 *>(src), static_cast<Vec8 *>(dst), nvec);
@@ -142,7 +142,7 @@ extern "C" int q3k_bench_stream_u128(const void *in0, const void *in1, void *out
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream pointers must be 16-byte aligned (in0, out0 non-null)");
     const int64_t nvec = bytes / 16;
     const int64_t blocks = (nvec + kBlock - 1) / kBlock;
-    if (blocks >= (int64_t{1} << 31))
+    if (!launch_fits(blocks, kBlock))
         return bench_error(Q3K_ERR_OVERFLOW, "stream size exceeds one launch");
     stream_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
         static_cast<const Vec8 *>(in0), static_cast<const Vec8 *>(in1), static_cast<Vec8 *>(out0),
@@ -167,7 +167,7 @@ extern "C" int q3k_bench_read_rows_u128(const void *base, const void *base2, int
     if (base == nullptr || sink == nullptr || !aligned16(base) || (base2 != nullptr && !aligned16(base2)) ||
         !aligned_to(sink, 4))
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "read pointers must be non-null and 16-byte aligned");
-    if (outer > INT32_MAX / inner)
+    if (outer > INT64_MAX / inner || !launch_fits(outer * inner, kBlock))
         return bench_error(Q3K_ERR_OVERFLOW, "read view count exceeds one launch");
     read_rows_kernel<<<dim3(static_cast<unsigned>(outer * inner)), dim3(kBlock), 0,
                        reinterpret_cast<hipStream_t>(stream)>>>(

@@ -80,6 +80,33 @@ def test_argument_errors_without_gpu(q3k):
     _expect(q3k.bench_read_rows, ValueError, IA, None, None, 2, 4096, 2, 256, 8, 512, 256, fake)
     _expect(q3k.bench_read_rows, ValueError, IA, fake, None, -1, 4096, 2, 256, 8, 512, 256, fake)
     q3k.bench_read_rows(None, None, 0, 4096, 2, 256, 8, 512, 256, None)
+    # grids past 2^32 - 1 work-items (256-thread blocks) are refused, not launched
+    _expect(q3k.bench_copy, OverflowError, OV, fake, fake, 16 * 256 * (2**24))
+    _expect(q3k.bench_stream, OverflowError, OV, fake, None, fake, None, 16 * 256 * (2**24))
+    q3k.bench_copy(None, None, 0)   # nothing to move: no launch
+    _expect(q3k.bench_read_rows, OverflowError, OV, fake, None, 2**13, 16, 2**11, 16, 1, 16, 16, fake)
+
+
+class _SizedFake:
+    """A buffer object that knows its size but is never dereferenced."""
+
+    def __init__(self, nbytes):
+        self.ptr, self.nbytes = 256, nbytes
+
+
+def test_bench_wrappers_refuse_buffers_smaller_than_the_call(q3k):
+    """The measurement aids' C ABI takes bare addresses; the Python wrappers check a sized buffer object against
+    the bytes the call reads or writes before calling it (the read kernel writes outer * inner * 256 words of
+    sink)."""
+    small, big = _SizedFake(1 << 20), _SizedFake(1 << 30)
+    with pytest.raises(ValueError, match="sink"):
+        q3k.bench_read_rows(big, None, 8, 1 << 20, 256, 256, 4, 2048, 256, small)   # 2048 views: 2 MiB of sink
+    with pytest.raises(ValueError, match="base"):
+        q3k.bench_read_rows(small, None, 64, 1 << 20, 8, 256, 4096, 2048, 256, big)
+    with pytest.raises(ValueError, match="destination"):
+        q3k.bench_copy(big, small, 1 << 21)
+    with pytest.raises(ValueError, match="out1"):
+        q3k.bench_stream(big, big, big, small, 1 << 21)
 
 
 def test_empty_inputs_are_no_ops(q3k):
