@@ -29,6 +29,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import importlib
 import importlib.util
 import json
@@ -597,6 +598,73 @@ def c5_extra(q3k, hip, synth, configs, stream, steps):
     return out
 
 
+def tp8_shard_extra(q3k, hip, synth, configs, stream, steps):
+    """Config 4 at one GPU's share under 8-way tensor parallelism, the shapes the sharding plan gives each rank
+    (the collectives themselves are not built): Q/K norm + RoPE on the rank's 4 query heads and 1 KV head of
+    every token, SwiGLU on its 1536 of the 12288 intermediate columns, and add + RMSNorm on its 1024-token slice
+    after the reduce-scatter (whole 4096-wide rows).  Per-op GB/s of algorithmic bytes, each op timed alone over
+    rotating inputs, and the three ops back to back."""
+    c = dataclasses.replace(configs.CONFIGS["c4"], name="c4-tp8-shard", heads_q=32 // 8, heads_kv=8 // 8,
+                            inter=12288 // 8)
+    T, H, I = c.tokens, c.hidden, c.inter
+    Ts = T // 8
+    s = c.seed
+    print("[bench] config 4 at a tensor-parallel-8 shard", file=sys.stderr, flush=True)
+    DB = hip.DeviceBuffer.from_array
+    base = {
+        "h1": DB(synth.normal_bf16(s, configs.TID_H, (Ts, H))),
+        "d1": DB(synth.normal_bf16(s, configs.TID_D1, (Ts, H))),
+        "w1": DB(synth.normal_bf16(s, configs.TID_W1, (H,), mean=1.0, std=0.1)),
+        "y1": hip.DeviceBuffer(Ts * H * 2),
+        "q": DB(synth.normal_bf16(s, configs.TID_Q, (T, c.heads_q * D))),
+        "k": DB(synth.normal_bf16(s, configs.TID_K, (T, c.heads_kv * D))),
+        "qw": DB(synth.normal_bf16(s, configs.TID_QW, (D,), mean=1.0, std=0.1)),
+        "kw": DB(synth.normal_bf16(s, configs.TID_KW, (D,), mean=1.0, std=0.1)),
+        "g": DB(synth.normal_bf16(s, configs.TID_GATE, (T, I))),
+        "u": DB(synth.normal_bf16(s, configs.TID_UP, (T, I))),
+        "o": hip.DeviceBuffer(T * I * 2),
+        "cache": DB(q3k.build_rope_cache(c.max_pos, D, configs.THETA)),
+    }
+    shared = ("w1", "qw", "kw", "cache")
+    sets = [base]
+    for _ in range(5):
+        st = clone_set(hip, {k: v for k, v in base.items() if k not in shared})
+        st.update({k: base[k] for k in shared})
+        sets.append(st)
+
+    def ops(b):
+        return [
+            ("add_rms_norm", lambda: q3k.add_rms_norm(b["h1"], b["d1"], b["w1"], b["y1"], Ts, H, EPS, stream)),
+            ("qk_norm_rope", lambda: q3k.qk_norm_rope(b["q"], b["k"], b["qw"], b["kw"], c.batch, c.seq, c.heads_q,
+                                                      c.heads_kv, D, EPS, b["cache"], c.max_pos, 0, None, stream)),
+            ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * I, stream)),
+        ]
+
+    reps = max(20, steps)
+    ms = time_chain(hip, stream, sets, ops, reps, 2)
+    per_op = time_each_op(hip, stream, sets, ops, reps,
+                          buffers={"add_rms_norm": ("h1", "d1", "y1"), "qk_norm_rope": ("q", "k"),
+                                   "silu_mul": ("g", "u", "o")})
+    op_bytes = {"add_rms_norm": configs.bytes_add_rms_norm(Ts, H),
+                "qk_norm_rope": configs.bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, D, c.distinct_positions()),
+                "silu_mul": configs.bytes_silu_mul(T, I)}
+    chain = sum(op_bytes.values())
+    out = {"shapes": {"add_rms_norm": [Ts, H], "q": [T, c.heads_q, D], "k": [T, c.heads_kv, D], "silu_mul": [T, I]},
+           "chain_bytes": chain, "chain_ms": round(ms, 5),
+           "chain_GB/s": round(chain / (ms * 1e-3) / 1e9, 1),
+           "chain_pct_of_peak": round(100 * chain / (ms * 1e-3) / 1e9 / PEAK_GBS, 2),
+           "per_op": {n: {"ms": round(t, 5), "bytes": op_bytes[n], "GB/s": round(op_bytes[n] / (t * 1e-3) / 1e9, 1),
+                          "pct_of_peak": round(100 * op_bytes[n] / (t * 1e-3) / 1e9 / PEAK_GBS, 2)}
+                      for n, t in per_op.items()}}
+    seen = set()
+    for st in sets:
+        for b in st.values():
+            if id(b) not in seen:
+                seen.add(id(b))
+                b.free()
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -804,6 +872,7 @@ def main():
                 b.free()
         extras["c3_decode"] = c3_decode_extra(q3k, hip, synth, configs, stream)
         extras["c5_prefill"] = c5_extra(q3k, hip, synth, configs, stream, args.steps)
+        extras["tp8_shard"] = tp8_shard_extra(q3k, hip, synth, configs, stream, args.steps)
     extras.update(child)
 
     cpu = None

@@ -213,7 +213,12 @@ namespace q3k
         // HGK.  Q is rewritten in place; K in place too, or with KV into the
         // cache rows given by `kv` (k itself is then only read).  Heads and
         // tokens are wave-uniform and below 2^31 (checked by the launcher).
-        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR>
+        // ANYH (a head count that is not a multiple of 4; HGQ = HGK = 1): lane
+        // group j of the tensor's wave w takes row 4 w + j of its flattened
+        // [tokens * heads] rows, so the four rows of a wave may belong to
+        // different tokens (token and position are then per lane group), and
+        // the groups past the last row of a partial last wave do nothing.
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, bool ANYH>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
@@ -224,6 +229,43 @@ namespace q3k
                                  __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             if (wave >= total_waves)
                 return;
+            if constexpr (ANYH)
+            {
+                static_assert(HGQ == 1 && HGK == 1, "one head per lane group");
+                const bool is_q = wave < q_waves;
+                const int32_t heads = is_q ? heads_q : heads_k;
+                const int64_t row = (is_q ? wave : wave - q_waves) * kHeadsPerWave + (threadIdx.x % kWave) / 16;
+                if (row >= rs.tokens * heads)
+                    return;
+                // rows and tokens are below 2^31 (checked by the launcher)
+                const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(heads);
+                const int64_t pos = token_position(rs, token);
+                const int64_t vec = row * kVecPerHead + threadIdx.x % 16;
+                if (is_q)
+                {
+                    Vec8 *p = reinterpret_cast<Vec8 *>(q) + vec;
+                    rope_heads<NORM, NTM, 1, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, pos, eps);
+                    return;
+                }
+                Vec8 *src = reinterpret_cast<Vec8 *>(k) + vec;
+                if constexpr (KV)
+                {
+                    const uint32_t seq = static_cast<uint32_t>(rs.seq);
+                    const uint32_t b = token / seq;
+                    const int64_t cache_row = static_cast<int64_t>(b) * kv.seq_cap + kv.cache_start + (token - b * seq);
+                    const int64_t dvec = (cache_row * heads_k + (row - static_cast<int64_t>(token) * heads_k)) *
+                                             kVecPerHead + threadIdx.x % 16;
+                    rope_heads<NORM, NTM, 1, true, PR>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + dvec,
+                                                       reinterpret_cast<const Vec8 *>(kv.v) + vec,
+                                                       reinterpret_cast<Vec8 *>(kv.v_cache) + dvec, kw, rs.cache, pos,
+                                                       eps);
+                }
+                else
+                {
+                    rope_heads<NORM, NTM, 1, false, PR>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
+                }
+                return;
+            }
             if (wave < q_waves)
             {
                 const uint32_t head0 = static_cast<uint32_t>(wave * kHeadsPerWave * HGQ);
@@ -288,7 +330,7 @@ namespace q3k
 
         bool fast_ok(const void *x, const float *cache, int32_t heads, int32_t head_dim)
         {
-            return head_dim == kHeadDim && heads % kHeadsPerWave == 0 && aligned16(x) && aligned16(cache);
+            return head_dim == kHeadDim && aligned16(x) && aligned16(cache);
         }
 
         void launch_generic_rope(uint16_t *x, int32_t heads, int32_t head_dim, const RopeShape &rs, hipStream_t stream)
@@ -334,14 +376,20 @@ namespace q3k
             return Q3K_OK;
         }
 
-        int64_t waves_for(int64_t tokens, int32_t heads, int hg) { return tokens * heads / (kHeadsPerWave * hg); }
+        // waves over the tensor's rows: whole when heads % (4 hg) == 0, the last
+        // one partial otherwise (ANYH, hg = 1)
+        int64_t waves_for(int64_t tokens, int32_t heads, int hg)
+        {
+            return (tokens * heads + kHeadsPerWave * hg - 1) / (kHeadsPerWave * hg);
+        }
+        bool any_heads(int32_t hq, int32_t hk) { return hq % kHeadsPerWave != 0 || hk % kHeadsPerWave != 0; }
 
         // Heads per lane: 4 when the head count allows it (32 or 64 query
         // heads), else 2 (8 KV heads), else 1.
         int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
         constexpr int64_t kSmallLaunchHeads = 16384; // below this many (token, head) rows: one head per lane group
 
-        template <bool NORM, bool KV, int HGQ, int HGK>
+        template <bool NORM, bool KV, int HGQ, int HGK, bool ANYH = false>
         void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
                              int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv, hipStream_t stream)
         {
@@ -349,8 +397,8 @@ namespace q3k
             const int64_t q_waves = waves_for(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads><<<dim3(blocks), dim3(kBlock), 0, stream>>>(
-                q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
+                <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
         template <bool NORM, bool KV = false>
@@ -360,6 +408,11 @@ namespace q3k
             // A small launch (decode: a few tokens) spreads one head per lane
             // group over more waves: fewer heads per wave shorten its serial
             // chain, and the waves fill more CUs.
+            if (any_heads(hq, k == nullptr ? 0 : hk))
+            {
+                launch_heads_hg<NORM, KV, 1, 1, true>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                return;
+            }
             const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kSmallLaunchHeads;
             const int gq = small ? 1 : heads_per_lane(hq);
             const int gk = small ? 1 : (k == nullptr ? gq : heads_per_lane(hk));
@@ -378,7 +431,16 @@ namespace q3k
             }
         }
 
-        bool grid_ok(int64_t tokens, int32_t heads) { return rope_heads_fit(tokens, heads); }
+        // every tensor's rows below 2^31, and the grid of the waves the launcher
+        // makes (each tensor's last wave may be partial) within the launch limit
+        bool grid_ok(int64_t tokens, int32_t hq, int32_t hk)
+        {
+            if (!rope_heads_fit(tokens, hq) || (hk > 0 && !rope_heads_fit(tokens, hk)) ||
+                !rope_heads_fit(tokens, hq + hk))
+                return false;
+            const int64_t waves = waves_for(tokens, hq, 1) + waves_for(tokens, hk, 1);
+            return launch_fits(blocks_for(waves, kWavesPerBlock), kBlock);
+        }
     } // namespace
 } // namespace q3k
 
@@ -394,7 +456,7 @@ extern "C" int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, i
         return Q3K_OK;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    if (fast_ok(x, cache, heads, D) && grid_ok(tokens, heads))
+    if (fast_ok(x, cache, heads, D) && grid_ok(tokens, heads, 0))
         launch_heads<false>(x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, s);
     else
         launch_generic_rope(x, heads, D, rs, s);
@@ -423,7 +485,7 @@ extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *q
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
     if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) &&
-        grid_ok(tokens, Hq + Hkv))
+        grid_ok(tokens, Hq, Hkv))
     {
         launch_heads<true>(q, k, qw, kw, Hq, Hkv, tokens, rs, eps, s);
         return check_launch("qk_norm_rope");
@@ -467,7 +529,7 @@ extern "C" int q3k_qk_norm_rope_kv_append_bf16(uint16_t *q, const uint16_t *k, c
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
     if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) && aligned16(v) &&
-        aligned16(k_cache) && aligned16(v_cache) && grid_ok(tokens, Hq + Hkv))
+        aligned16(k_cache) && aligned16(v_cache) && grid_ok(tokens, Hq, Hkv))
     {
         const KvDest kv{v, k_cache, v_cache, seq_cap, cache_start};
         launch_heads<true, true>(q, const_cast<uint16_t *>(k), qw, kw, Hq, Hkv, tokens, rs, eps, s, kv);

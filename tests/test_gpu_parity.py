@@ -227,7 +227,10 @@ def test_rope_kat(q3k, hip, oracle):
 @pytest.mark.parametrize("B,S,heads,D,start,offset", [(1, 64, 16, 128, 0, 0), (2, 33, 8, 128, 100, 0),
                                                       (4, 16, 32, 128, 7, 0), (1, 5, 2, 128, 0, 0),
                                                       (2, 9, 4, 64, 3, 0), (1, 7, 8, 128, 0, 2),
-                                                      (3, 4, 6, 128, 1, 0)])
+                                                      (3, 4, 6, 128, 1, 0),
+                                                      # head counts that are not a multiple of 4: waves span tokens,
+                                                      # and the last wave is partial
+                                                      (3, 7, 1, 128, 2, 0), (2, 5, 3, 128, 0, 0)])
 def test_rope_shapes(q3k, hip, oracle, synth, B, S, heads, D, start, offset):
     name = f"rope B={B} S={S} heads={heads} D={D} start={start} offset={offset}"
     announce(name)
@@ -255,7 +258,13 @@ def test_rope_positions_overload(q3k, hip, oracle, synth):
 @pytest.mark.parametrize("B,S,Hq,Hkv,D,start,offset", [(1, 512, 16, 8, 128, 0, 0), (4, 64, 32, 8, 128, 0, 0),
                                                        (2, 32, 64, 8, 128, 5, 0), (1, 3, 2, 1, 8, 5, 0),
                                                        (2, 5, 6, 2, 128, 0, 0), (1, 8, 4, 4, 128, 0, 2),
-                                                       (1, 4, 4, 4, 64, 2, 0)])
+                                                       (1, 4, 4, 4, 64, 2, 0),
+                                                       # config 4 at one rank of 8-way tensor parallelism (4 query
+                                                       # heads, 1 KV head), full size; other head counts that are
+                                                       # not a multiple of 4, with partial last waves
+                                                       (4, 2048, 4, 1, 128, 0, 0), (3, 7, 5, 3, 128, 1, 0),
+                                                       (1, 9, 4, 1, 128, 0, 0), (2, 3, 1, 1, 128, 0, 0),
+                                                       (1, 11, 2, 2, 128, 4, 0)])
 def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, offset):
     name = f"qk_norm_rope B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} start={start} offset={offset}"
     announce(name)
@@ -481,6 +490,8 @@ def test_kv_append_shapes(q3k, hip, oracle, synth, B, S, row, Bc, Sc, start, dty
     (2, 12, 64, 4, 128, 12, 0, None, 0),       # Qwen3-32B shape, whole capacity
     (2, 7, 4, 2, 64, 12, 3, None, 0),          # head_dim 64: generic path
     (2, 5, 8, 4, 128, 8, 2, None, 2),          # unaligned: generic path
+    (2, 17, 4, 1, 128, 40, 5, None, 0),        # one rank of 8-way tensor parallelism: 4 query heads, 1 KV head
+    (3, 9, 6, 2, 128, 16, 0, "random", 0),     # 6 and 2 heads, per-token positions, one outside the table
 ])
 def test_qk_norm_rope_kv_append(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, Sc, cs, positions, offset):
     """Fused Q/K norm + RoPE + KV append (self_attention.cpp:147-156) against the oracle composition, and bit for
