@@ -8,7 +8,9 @@
 // of that group, so every K/V tile it stages in LDS serves G heads.  (A
 // decode step with its key range split into short slices runs the same code
 // as one-wave blocks, one slice each.)  A wave's
-// 32 "columns" are (position, head) pairs.  Per 32 keys:
+// 32 "columns" are (position, head) pairs: floor(32 / G) positions of the G
+// heads (any G up to 32; a G that does not divide 32, such as Qwen3-14B's 5,
+// leaves 32 mod G padding columns).  Per 32 keys:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16: A = K rows from LDS,
 //                 B = the wave's Q fragments (registers for the whole loop);
 //   online softmax per column: a lane holds one column, so the key max and
@@ -429,11 +431,16 @@ namespace q3k
 
         // ---- the matrix-core kernel ---------------------------------------------
 
+        // G is the group size Hq / Hkv, or 0 for a group size that does not
+        // divide 32 (taken from the arguments at run time): a wave then holds
+        // floor(32 / G) positions of G heads, and its last 32 mod G columns are
+        // padding, computed like a padding column past S and never stored.
         template <int G, int WAVES>
         __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnArgs a)
         {
-            constexpr int PW = 32 / G;         // query positions per wave
-            constexpr int QP = WAVES * PW;     // per block
+            const int g = G > 0 ? G : a.Hq / a.Hkv;
+            const int PW = 32 / g;             // query positions per wave
+            const int QP = WAVES * PW;         // per block
             // K and V tiles, two buffers each.  Tile t's P V product is issued in
             // step t + 1, beside the softmax of tile t + 1, so V(t) stays resident
             // one step longer than K(t); V(t + 1) is loaded into V(t - 1)'s buffer
@@ -476,9 +483,9 @@ namespace q3k
 
             // this lane's column
             const int32_t wave_s0 = s0 + wave * PW;
-            const int32_t s_col = wave_s0 + li / G;
-            const int h_col = kvh * G + li % G;
-            const bool col_ok = s_col < S;
+            const int32_t s_col = wave_s0 + li / g;
+            const int h_col = kvh * g + li % g;
+            const bool col_ok = s_col < S && li < PW * g;
             const int32_t last_key = start + s_col;
             const bool wave_active = wave_s0 < S;
             const bool wave_partial = wave_s0 + PW > S;
@@ -685,7 +692,7 @@ namespace q3k
 
         bool mfma_ok(const AttnArgs &a, int32_t G)
         {
-            const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32;
+            const bool g_ok = G >= 1 && G <= 32;
             // tile loads use 32-bit byte offsets of up to kKeyTile rows
             const int64_t row_limit = (INT32_MAX - kRowBytes) / (2 * kKeyTile);
             return g_ok && a.D == kAttD && a.start + a.S <= INT32_MAX && a.ks1 <= row_limit && a.vs1 <= row_limit &&
@@ -743,7 +750,7 @@ namespace q3k
         template <int G>
         int launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
         {
-            constexpr int QP = kAttWaves * (32 / G);
+            const int QP = kAttWaves * (32 / (G > 0 ? G : a.Hq / a.Hkv));
             a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
             if (!launch_fits(blocks, kAttBlock) || (a.splits > 1 && !launch_fits(a.rows, kCombineWaves * kWave)))
@@ -751,7 +758,7 @@ namespace q3k
             if (a.splits > 1 && a.S == 1 && a.split_keys <= kMaxOneWaveSplitKeys)
             {
                 // one query position per block either way (QP >= 1), so the grid is the same
-                static_assert(32 / G >= 1, "one position per wave at least");
+                static_assert(G == 0 || 32 / G >= 1, "one position per wave at least");
                 attn_mfma_kernel<G, 1><<<dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream>>>(a);
             }
             else
@@ -841,7 +848,8 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
         case 4: return launch_mfma<4>(a, B, s);
         case 8: return launch_mfma<8>(a, B, s);
         case 16: return launch_mfma<16>(a, B, s);
-        default: return launch_mfma<32>(a, B, s);
+        case 32: return launch_mfma<32>(a, B, s);
+        default: return launch_mfma<0>(a, B, s);
         }
     }
     const int64_t rows = B * S * Hq;

@@ -601,6 +601,12 @@ def test_attention_kat(q3k, hip, oracle):
     (1, 45, 7, 64, 8, 128, 60, 0),      # G = 8
     (1, 20, 3, 32, 2, 128, 30, 0),      # G = 16
     (1, 9, 60, 32, 1, 128, 70, 0),      # G = 32
+    # group sizes that do not divide 32: padding columns in every wave
+    (2, 77, 13, 40, 8, 128, 100, 0),    # Qwen3-14B heads (G = 5), prefill with a cached prefix
+    (8, 1, 300, 40, 8, 128, 512, 0),    # G = 5 decode step
+    (1, 50, 0, 24, 8, 128, 50, 0),      # G = 3
+    (2, 33, 6, 12, 2, 128, 40, 0),      # G = 6
+    (1, 20, 2, 20, 1, 128, 24, 0),      # G = 20: one position per wave
 ])
 def test_gqa_attention(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, D, cap, offset):
     name = f"gqa_attention B={B} S={S} start={start} Hq={Hq} Hkv={Hkv} D={D} cap={cap} offset={offset}"
@@ -690,7 +696,8 @@ def test_bench_stream(q3k, hip, n_in, n_out, in_place):
         check_exact("bench_stream in1 unchanged", B.get(np.uint32, (n // 4,)), b)
 
 
-@pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128), (1, 8192, 64, 8, 192)])
+@pytest.mark.parametrize("B,S,Hq,Hkv,nrows", [(4, 2048, 32, 8, 384), (1, 4096, 32, 8, 128), (1, 8192, 64, 8, 192),
+                                               (2, 2048, 40, 8, 192)])
 def test_gqa_attention_prefill_sampled(q3k, hip, oracle, synth, B, S, Hq, Hkv, nrows):
     """Benchmark-size prefill (config 4 shape, a 4096-token sequence, and one 8192-token sequence of the config-5
     model's 64 query heads over 8 KV heads): every row computed on the GPU, a seeded sample of rows (always
@@ -865,7 +872,8 @@ def test_topk_candidates_ties(q3k, hip, oracle, synth, rows, N, k, levels, split
                                                  (1, 1, 300, 64, 8, 320), (1, 3, 400, 16, 8, 420),
                                                  (4, 1, 1000, 32, 8, 1100), (1, 1, 1000, 8, 8, 1100),
                                                  (1, 1, 500, 16, 8, 512), (2, 1, 900, 32, 2, 1000),
-                                                 (1, 1, 2000, 32, 1, 2100), (3, 1, 129, 32, 8, 200)])
+                                                 (1, 1, 2000, 32, 1, 2100), (3, 1, 129, 32, 8, 200),
+                                                 (1, 1, 4095, 40, 8, 4096), (2, 3, 600, 40, 8, 700)])
 def test_gqa_attention_split_keys(q3k, hip, oracle, synth, B, S, start, Hq, Hkv, cap):
     """Decode with few sequences: the key range is split across blocks (the workspace the library asks for) and the
     slices merged; same band as the single-pass kernel.  Decode steps whose slices hold one or two tiles run as
