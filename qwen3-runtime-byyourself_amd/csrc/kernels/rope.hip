@@ -68,6 +68,21 @@ namespace q3k
             return (pos >= 0 && pos < rs.table_positions) ? pos : -1;
         }
 
+        // token_position for a per-lane token, in 32-bit arithmetic (tokens and
+        // the sequence length are below 2^31)
+        __device__ __forceinline__ int64_t lane_token_position(const RopeShape &rs, uint32_t token)
+        {
+            int64_t pos;
+            if (rs.positions != nullptr)
+                pos = rs.positions[token];
+            else
+            {
+                const uint32_t seq = static_cast<uint32_t>(rs.seq);
+                pos = rs.start + (token - token / seq * seq);
+            }
+            return (pos >= 0 && pos < rs.table_positions) ? pos : -1;
+        }
+
         // Where the K (and V) heads of the fused KV-cache append go: token
         // t = b * S + s of the input lands in row b * seq_cap + cache_start + s
         // of the layer's [batch_cap, seq_cap, Hkv, D] cache.  V is copied
@@ -213,12 +228,13 @@ namespace q3k
         // HGK.  Q is rewritten in place; K in place too, or with KV into the
         // cache rows given by `kv` (k itself is then only read).  Heads and
         // tokens are wave-uniform and below 2^31 (checked by the launcher).
-        // ANYH (a head count that is not a multiple of 4; HGQ = HGK = 1): lane
-        // group j of the tensor's wave w takes row 4 w + j of its flattened
-        // [tokens * heads] rows, so the four rows of a wave may belong to
-        // different tokens (token and position are then per lane group), and
-        // the groups past the last row of a partial last wave do nothing.
-        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, bool ANYH>
+        // ANYH bit 0 (Q) / bit 1 (K): that tensor's head count is not a
+        // multiple of 4 (with HGQ = HGK = 1).  Lane group j of the tensor's
+        // wave w then takes row 4 w + j of its flattened [tokens * heads]
+        // rows, so the four rows of a wave may belong to different tokens
+        // (token and position are per lane group), and the groups past the
+        // last row of a partial last wave do nothing.
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, int ANYH>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
@@ -229,42 +245,47 @@ namespace q3k
                                  __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             if (wave >= total_waves)
                 return;
-            if constexpr (ANYH)
+            if constexpr (ANYH != 0)
             {
                 static_assert(HGQ == 1 && HGK == 1, "one head per lane group");
                 const bool is_q = wave < q_waves;
-                const int32_t heads = is_q ? heads_q : heads_k;
-                const int64_t row = (is_q ? wave : wave - q_waves) * kHeadsPerWave + (threadIdx.x % kWave) / 16;
-                if (row >= rs.tokens * heads)
+                if ((is_q && (ANYH & 1)) || (!is_q && (ANYH & 2)))
+                {
+                    const int32_t heads = is_q ? heads_q : heads_k;
+                    const int64_t row = (is_q ? wave : wave - q_waves) * kHeadsPerWave + (threadIdx.x % kWave) / 16;
+                    if (row >= rs.tokens * heads)
+                        return;
+                    // rows, tokens and the sequence length are below 2^31
+                    // (checked by the launcher): 32-bit index arithmetic
+                    const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(heads);
+                    const int64_t pos = lane_token_position(rs, token);
+                    const int64_t vec = row * kVecPerHead + threadIdx.x % 16;
+                    if (is_q)
+                    {
+                        Vec8 *p = reinterpret_cast<Vec8 *>(q) + vec;
+                        rope_heads<NORM, NTM, 1, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, pos, eps);
+                        return;
+                    }
+                    Vec8 *src = reinterpret_cast<Vec8 *>(k) + vec;
+                    if constexpr (KV)
+                    {
+                        const uint32_t seq = static_cast<uint32_t>(rs.seq);
+                        const uint32_t b = token / seq;
+                        const int64_t cache_row =
+                            static_cast<int64_t>(b) * kv.seq_cap + kv.cache_start + (token - b * seq);
+                        const int64_t dvec = (cache_row * heads_k + (row - static_cast<int64_t>(token) * heads_k)) *
+                                                 kVecPerHead + threadIdx.x % 16;
+                        rope_heads<NORM, NTM, 1, true, PR>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + dvec,
+                                                           reinterpret_cast<const Vec8 *>(kv.v) + vec,
+                                                           reinterpret_cast<Vec8 *>(kv.v_cache) + dvec, kw, rs.cache,
+                                                           pos, eps);
+                    }
+                    else
+                    {
+                        rope_heads<NORM, NTM, 1, false, PR>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
+                    }
                     return;
-                // rows and tokens are below 2^31 (checked by the launcher)
-                const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(heads);
-                const int64_t pos = token_position(rs, token);
-                const int64_t vec = row * kVecPerHead + threadIdx.x % 16;
-                if (is_q)
-                {
-                    Vec8 *p = reinterpret_cast<Vec8 *>(q) + vec;
-                    rope_heads<NORM, NTM, 1, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, pos, eps);
-                    return;
                 }
-                Vec8 *src = reinterpret_cast<Vec8 *>(k) + vec;
-                if constexpr (KV)
-                {
-                    const uint32_t seq = static_cast<uint32_t>(rs.seq);
-                    const uint32_t b = token / seq;
-                    const int64_t cache_row = static_cast<int64_t>(b) * kv.seq_cap + kv.cache_start + (token - b * seq);
-                    const int64_t dvec = (cache_row * heads_k + (row - static_cast<int64_t>(token) * heads_k)) *
-                                             kVecPerHead + threadIdx.x % 16;
-                    rope_heads<NORM, NTM, 1, true, PR>(src, reinterpret_cast<Vec8 *>(kv.k_cache) + dvec,
-                                                       reinterpret_cast<const Vec8 *>(kv.v) + vec,
-                                                       reinterpret_cast<Vec8 *>(kv.v_cache) + dvec, kw, rs.cache, pos,
-                                                       eps);
-                }
-                else
-                {
-                    rope_heads<NORM, NTM, 1, false, PR>(src, src, nullptr, nullptr, kw, rs.cache, pos, eps);
-                }
-                return;
             }
             if (wave < q_waves)
             {
@@ -389,7 +410,7 @@ namespace q3k
         int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
         constexpr int64_t kSmallLaunchHeads = 16384; // below this many (token, head) rows: one head per lane group
 
-        template <bool NORM, bool KV, int HGQ, int HGK, bool ANYH = false>
+        template <bool NORM, bool KV, int HGQ, int HGK, int ANYH = 0>
         void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
                              int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv, hipStream_t stream)
         {
@@ -410,7 +431,14 @@ namespace q3k
             // chain, and the waves fill more CUs.
             if (any_heads(hq, k == nullptr ? 0 : hk))
             {
-                launch_heads_hg<NORM, KV, 1, 1, true>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                // per-lane rows only for the tensor whose head count needs them
+                const int any = (hq % kHeadsPerWave != 0 ? 1 : 0) | (k != nullptr && hk % kHeadsPerWave != 0 ? 2 : 0);
+                if (any == 1)
+                    launch_heads_hg<NORM, KV, 1, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                else if (any == 2)
+                    launch_heads_hg<NORM, KV, 1, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                else
+                    launch_heads_hg<NORM, KV, 1, 1, 3>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 return;
             }
             const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kSmallLaunchHeads;
