@@ -4,13 +4,13 @@
 // 0 .. start + s, query head h reads KV head h / (Hq / Hkv)).
 //
 // Matrix-core path (head_dim 128, unit dim stride, 16-byte rows): a block of
-// four waves owns one (batch, KV head) and QP query positions of all G heads
-// of that group, so every K/V tile it stages in LDS serves G heads.  (A
+// four waves owns one (batch, KV head) and 128 of its (position, head)
+// columns, so every K/V tile it stages in LDS serves 128 query rows.  (A
 // decode step with its key range split into short slices runs the same code
 // as one-wave blocks, one slice each.)  A wave's
-// 32 "columns" are (position, head) pairs: floor(32 / G) positions of the G
-// heads (any G up to 32; a G that does not divide 32, such as Qwen3-14B's 5,
-// leaves 32 mod G padding columns).  Per 32 keys:
+// 32 "columns" are consecutive (position, head) pairs in position-major
+// order: 32 / G whole positions when G divides 32; any G up to 32 works (for
+// Qwen3-14B's 5 a position's heads may straddle two waves).  Per 32 keys:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16: A = K rows from LDS,
 //                 B = the wave's Q fragments (registers for the whole loop);
 //   online softmax per column: a lane holds one column, so the key max and
@@ -432,15 +432,16 @@ namespace q3k
         // ---- the matrix-core kernel ---------------------------------------------
 
         // G is the group size Hq / Hkv, or 0 for a group size that does not
-        // divide 32 (taken from the arguments at run time): a wave then holds
-        // floor(32 / G) positions of G heads, and its last 32 mod G columns are
-        // padding, computed like a padding column past S and never stored.
+        // divide 32 (taken from the arguments at run time).  The S * G columns
+        // of one (batch, KV head), (position, head) pairs in position-major
+        // order, go 32 to a wave and 32 * WAVES to a block; for a G that
+        // divides 32 a wave thus holds 32 / G whole positions, otherwise a
+        // position's heads may straddle two waves or blocks.
         template <int G, int WAVES>
         __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnArgs a)
         {
             const int g = G > 0 ? G : a.Hq / a.Hkv;
-            const int PW = 32 / g;             // query positions per wave
-            const int QP = WAVES * PW;         // per block
+            constexpr int kBlockCols = 32 * WAVES;
             // K and V tiles, two buffers each.  Tile t's P V product is issued in
             // step t + 1, beside the softmax of tile t + 1, so V(t) stays resident
             // one step longer than K(t); V(t + 1) is loaded into V(t - 1)'s buffer
@@ -470,10 +471,13 @@ namespace q3k
             bid /= a.qblocks;
             const int kvh = bid % a.Hkv;
             const int64_t b = bid / a.Hkv;
-            // positions and key indices fit in 32 bits (checked by the launcher)
+            // positions, columns and key indices fit in 32 bits (checked by the
+            // launcher: B * S * Hq < 2^31)
             const int32_t S = static_cast<int32_t>(a.S), start = static_cast<int32_t>(a.start);
-            const int32_t s0 = qb * QP;
-            const int32_t s_last = (s0 + QP < S ? s0 + QP : S) - 1;
+            const int32_t n_cols = S * g;
+            const int64_t block_col = static_cast<int64_t>(qb) * kBlockCols;
+            const int32_t block_end = static_cast<int32_t>(block_col + kBlockCols < n_cols ? block_col + kBlockCols : n_cols);
+            const int32_t s_last = (block_end - 1) / g;
             const int32_t n_keys = start + s_last + 1;
             // this block's key slice [sp * split_keys, ...) within the causal range
             const int32_t k_begin = sp * a.split_keys;
@@ -482,13 +486,15 @@ namespace q3k
             const int ntiles = k_end > k_begin ? (k_end + kKeyTile - 1) / kKeyTile : tile_begin;
 
             // this lane's column
-            const int32_t wave_s0 = s0 + wave * PW;
-            const int32_t s_col = wave_s0 + li / g;
-            const int h_col = kvh * g + li % g;
-            const bool col_ok = s_col < S && li < PW * g;
+            const int64_t wave_col = block_col + 32 * wave;
+            const int64_t col = wave_col + li;
+            const int32_t wave_s0 = static_cast<int32_t>(wave_col / g);  // the wave's first position
+            const int32_t s_col = static_cast<int32_t>(col / g);
+            const int h_col = kvh * g + static_cast<int>(col % g);
+            const bool col_ok = col < n_cols;
             const int32_t last_key = start + s_col;
-            const bool wave_active = wave_s0 < S;
-            const bool wave_partial = wave_s0 + PW > S;
+            const bool wave_active = wave_col < n_cols;
+            const bool wave_partial = wave_col + 32 > n_cols;
 
             bf16x8_t qf[kAttD / 16];
             load_q(a, b, s_col, h_col, col_ok, lg, qf);
@@ -724,8 +730,8 @@ namespace q3k
         {
             SplitPlan p;
             const int32_t G = Hq / Hkv;
-            const int64_t QP = kAttWaves * (32 / (G > 32 ? 32 : G));
-            const int64_t blocks = B * Hkv * ((S + QP - 1) / QP);
+            const int64_t cols = S * G, block_cols = 32 * kAttWaves;
+            const int64_t blocks = B * Hkv * ((cols + block_cols - 1) / block_cols);
             const int32_t min_keys = S == 1 ? kMinDecodeSplitKeys : kMinSplitKeys;
             if (blocks >= kSplitTargetBlocks || cached < 2 * min_keys)
                 return p;
@@ -750,14 +756,14 @@ namespace q3k
         template <int G>
         int launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
         {
-            const int QP = kAttWaves * (32 / (G > 0 ? G : a.Hq / a.Hkv));
-            a.qblocks = static_cast<int32_t>((a.S + QP - 1) / QP);
+            const int64_t cols = a.S * (a.Hq / a.Hkv), block_cols = 32 * kAttWaves;
+            a.qblocks = static_cast<int32_t>((cols + block_cols - 1) / block_cols);
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
             if (!launch_fits(blocks, kAttBlock) || (a.splits > 1 && !launch_fits(a.rows, kCombineWaves * kWave)))
                 return set_error(Q3K_ERR_OVERFLOW, "GQA grid is too large");
             if (a.splits > 1 && a.S == 1 && a.split_keys <= kMaxOneWaveSplitKeys)
             {
-                // one query position per block either way (QP >= 1), so the grid is the same
+                // one query position (at most 32 columns) per block either way, so the grid is the same
                 static_assert(G == 0 || 32 / G >= 1, "one position per wave at least");
                 attn_mfma_kernel<G, 1><<<dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream>>>(a);
             }
