@@ -250,26 +250,29 @@ def attention_flops(B, S, start, Hq, D):
 def time_attention(q3k, hip, synth, c, stream):
     """Grouped-query attention over the layer's KV cache (gqa_attention.cu:304-345): prefill at the config's
     [B, S] (matrix-core bound, reported in TFLOP/s against the 2.5 PFLOP/s bf16 peak) and a batched decode step
-    at 64 sequences x 4096 cached keys (HBM bound: the K/V cache is read once)."""
+    at 64 sequences x 4096 cached keys (HBM bound: the K/V cache is read once).  The prefill is also timed with
+    Qwen3-14B's 40 query heads over 8 KV heads (a group size of 5, which does not divide a wave's 32 columns)."""
     out = {}
     print("[bench] timing attention", file=sys.stderr, flush=True)
-    for name, B, S, start in (("prefill", c.batch, c.seq, 0), ("decode_b64_l4096", 64, 1, 4095),
-                              ("decode_b1_l4096", 1, 1, 4095)):
+    for name, B, S, start, Hq, Hkv in (("prefill", c.batch, c.seq, 0, c.heads_q, c.heads_kv),
+                                       ("prefill_40q_8kv", c.batch, c.seq, 0, 40, 8),
+                                       ("decode_b64_l4096", 64, 1, 4095, c.heads_q, c.heads_kv),
+                                       ("decode_b1_l4096", 1, 1, 4095, c.heads_q, c.heads_kv)):
         L = start + S
-        q = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 40, (B, S, c.heads_q * D)))
-        kc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 41, (B, L, c.heads_kv, D)))
-        vc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 42, (B, L, c.heads_kv, D)))
-        o = hip.DeviceBuffer(B * S * c.heads_q * D * 2)
-        st = (L * c.heads_kv * D, c.heads_kv * D, D, 1)
-        wb = q3k.gqa_attention_workspace_bytes(B, S, c.heads_q, c.heads_kv, D, L)
+        q = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 40, (B, S, Hq * D)))
+        kc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 41, (B, L, Hkv, D)))
+        vc = hip.DeviceBuffer.from_array(synth.normal_bf16(c.seed, 42, (B, L, Hkv, D)))
+        o = hip.DeviceBuffer(B * S * Hq * D * 2)
+        st = (L * Hkv * D, Hkv * D, D, 1)
+        wb = q3k.gqa_attention_workspace_bytes(B, S, Hq, Hkv, D, L)
         ws = hip.DeviceBuffer(wb) if wb else None   # a launch too small for the GPU splits the key range
         ms = time_chain(hip, stream, [0], lambda _: [
-            ("attention", lambda: q3k.gqa_attention(q, kc, vc, o, B, S, c.heads_q, c.heads_kv, D, L, start, st, st,
+            ("attention", lambda: q3k.gqa_attention(q, kc, vc, o, B, S, Hq, Hkv, D, L, start, st, st,
                                                     stream, workspace=ws, workspace_bytes=wb))],
                         50, 50 if S > 1 else 5)
-        flops = attention_flops(B, S, start, c.heads_q, D)
-        byts = 2 * B * L * c.heads_kv * D * 2 + 2 * B * S * c.heads_q * D * 2
-        rec = {"ms": round(ms, 5), "B": B, "S": S, "cached": L, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+        flops = attention_flops(B, S, start, Hq, D)
+        byts = 2 * B * L * Hkv * D * 2 + 2 * B * S * Hq * D * 2
+        rec = {"ms": round(ms, 5), "B": B, "S": S, "cached": L, "heads_q": Hq, "heads_kv": Hkv, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
                "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
         if S > 1:
             rec["pct_of_bf16_peak"] = round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
@@ -278,11 +281,11 @@ def time_attention(q3k, hip, synth, c, stream):
             if B >= 64:
                 # the same K/V rows read by a kernel that only reads them: the HBM
                 # ceiling of this access pattern at this grid
-                sink = hip.DeviceBuffer(B * c.heads_kv * 256 * 4)
+                sink = hip.DeviceBuffer(B * Hkv * 256 * 4)
                 ms_r = time_chain(hip, stream, [0], lambda _: [("read", lambda: q3k.bench_read_rows(
-                    kc, vc, B, L * c.heads_kv * D * 2, c.heads_kv, D * 2, L, c.heads_kv * D * 2, D * 2, sink,
+                    kc, vc, B, L * Hkv * D * 2, Hkv, D * 2, L, Hkv * D * 2, D * 2, sink,
                     stream))], 50, 2)
-                kv_bytes = 2 * B * L * c.heads_kv * D * 2
+                kv_bytes = 2 * B * L * Hkv * D * 2
                 rec["read_ceiling_GB/s"] = round(kv_bytes / (ms_r * 1e-3) / 1e9, 1)
                 rec["pct_of_read_ceiling"] = round(100 * ms_r / ms, 1)
                 sink.free()
