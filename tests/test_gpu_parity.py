@@ -264,7 +264,7 @@ def test_rope_positions_overload(q3k, hip, oracle, synth):
                                                        # not a multiple of 4, with partial last waves
                                                        (4, 2048, 4, 1, 128, 0, 0), (3, 7, 5, 3, 128, 1, 0),
                                                        (1, 9, 4, 1, 128, 0, 0), (2, 3, 1, 1, 128, 0, 0),
-                                                       (1, 11, 2, 2, 128, 4, 0)])
+                                                       (1, 11, 2, 2, 128, 4, 0), (2, 9, 6, 4, 128, 3, 0)])
 def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, offset):
     name = f"qk_norm_rope B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} start={start} offset={offset}"
     announce(name)
@@ -492,6 +492,7 @@ def test_kv_append_shapes(q3k, hip, oracle, synth, B, S, row, Bc, Sc, start, dty
     (2, 5, 8, 4, 128, 8, 2, None, 2),          # unaligned: generic path
     (2, 17, 4, 1, 128, 40, 5, None, 0),        # one rank of 8-way tensor parallelism: 4 query heads, 1 KV head
     (3, 9, 6, 2, 128, 16, 0, "random", 0),     # 6 and 2 heads, per-token positions, one outside the table
+    (2, 5, 6, 4, 128, 8, 1, None, 0),          # per-lane rows for Q only (6 heads), K (4 heads) wave-uniform
 ])
 def test_qk_norm_rope_kv_append(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, Sc, cs, positions, offset):
     """Fused Q/K norm + RoPE + KV append (self_attention.cpp:147-156) against the oracle composition, and bit for
