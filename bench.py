@@ -21,8 +21,12 @@ its buffers whose cycle exceeds 1.5 GiB (so none is served from the cache).
 
 Also reported (not part of ``value``): the embedding gather and the final
 RMSNorm at config 4, the same chain built from the unfused drop-in ops in
-the reference's order, a 128-bit copy ceiling, and the CPU baseline (the
-oracle's restatement of the reference's CPU arithmetic, timed on this host).
+the reference's order, each op's own access-pattern ceiling at its size, a
+128-bit copy ceiling, the other benchmark configs (1: RMSNorm [16, 1024];
+2: the Qwen3-0.6B chain with its embedding gather; 3: the decode step; 5:
+Qwen3-32B shapes), attention, token selection, weight IO, and the CPU
+baseline (the oracle's restatement of the reference's CPU arithmetic, timed
+on this host).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
 """
@@ -85,6 +89,9 @@ def make_chain_set(hip, synth, configs, c, q3k, seed_shift=0):
         "g": DB(synth.normal_bf16(s, configs.TID_GATE, (T, I))),
         "u": DB(synth.normal_bf16(s, configs.TID_UP, (T, I))),
         "o": hip.DeviceBuffer(T * I * 2),
+        # the unfused chain's normalised Q and K (rms_norm returns new tensors, self_attention.cpp:147-149)
+        "qn": hip.DeviceBuffer(T * c.heads_q * D * 2),
+        "kn": hip.DeviceBuffer(T * c.heads_kv * D * 2),
         "cache": DB(q3k.build_rope_cache(c.max_pos, D, configs.THETA)),
     }
     if c.positions == "uniform":   # one position per sequence (config 3): the Int32 positions overload
@@ -119,10 +126,12 @@ def unfused_ops(q3k, c, b, stream):
     return [
         ("add_inplace", lambda: q3k.add_inplace(b["h1"], b["d1"], T * H, stream)),
         ("rms_norm", lambda: q3k.rms_norm(b["h1"], b["w1"], b["y1"], T, H, EPS, stream)),
-        ("rms_norm_q", lambda: q3k.rms_norm(b["q"], b["qw"], b["o"], T * c.heads_q, D, EPS, stream)),
-        ("rms_norm_k", lambda: q3k.rms_norm(b["k"], b["kw"], b["y2"], T * c.heads_kv, D, EPS, stream)),
-        ("rope_q", lambda: q3k.rope(b["o"], c.batch, c.seq, c.heads_q, D, b["cache"], c.max_pos, 0, None, stream)),
-        ("rope_k", lambda: q3k.rope(b["y2"], c.batch, c.seq, c.heads_kv, D, b["cache"], c.max_pos, 0, None, stream)),
+        ("rms_norm_q", lambda: q3k.rms_norm(b["q"], b["qw"], b["qn"], T * c.heads_q, D, EPS, stream)),
+        ("rms_norm_k", lambda: q3k.rms_norm(b["k"], b["kw"], b["kn"], T * c.heads_kv, D, EPS, stream)),
+        # apply_rope_inplace on the normalised Q and K: one launch over both (the reference makes two,
+        # rope.cu:326-332)
+        ("rope", lambda: q3k.rope_qk(b["qn"], b["kn"], c.batch, c.seq, c.heads_q, c.heads_kv, D, b["cache"],
+                                     c.max_pos, 0, b.get("pos"), stream)),
         ("add_inplace_2", lambda: q3k.add_inplace(b["h2"], b["d2"], T * H, stream)),
         ("rms_norm_2", lambda: q3k.rms_norm(b["h2"], b["w2"], b["y2"], T, H, EPS, stream)),
         ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * c.inter, stream)),
@@ -185,8 +194,8 @@ OP_BUFFERS = {
     "silu_mul": ("g", "u", "o"),
 }
 UNFUSED_BUFFERS = {
-    "add_inplace": ("h1", "d1"), "rms_norm": ("h1", "y1"), "rms_norm_q": ("q",), "rms_norm_k": ("k",),
-    "rope_q": ("o",), "rope_k": ("y2",), "add_inplace_2": ("h2", "d2"), "rms_norm_2": ("h2", "y2"),
+    "add_inplace": ("h1", "d1"), "rms_norm": ("h1", "y1"), "rms_norm_q": ("q", "qn"), "rms_norm_k": ("k", "kn"),
+    "rope": ("qn", "kn"), "add_inplace_2": ("h2", "d2"), "rms_norm_2": ("h2", "y2"),
     "silu_mul": ("g", "u", "o"),
 }
 MIN_CYCLE_BYTES = 3 << 29  # 1.5 GiB: 6x the 256 MB Infinity Cache
@@ -544,6 +553,111 @@ def c3_decode_extra(q3k, hip, synth, configs, stream):
     return out
 
 
+def c1_extra(q3k, hip, synth, configs, stream):
+    """Config 1 (RMSNorm [16, 1024], the reference test's shape, tests/unit/rms_norm_cuda_test.cpp:174-244) on the
+    GPU: microseconds per call launched back to back and replayed from a HIP graph, over 8 copies of the inputs
+    (a 67 KB launch: latency, not bandwidth).  The CPU baseline times the same config with the reference test's
+    own loop (cpu_baseline.c1)."""
+    c = configs.CONFIGS["c1"]
+    T, H = c.tokens, c.hidden
+    print("[bench] config 1 rms_norm", file=sys.stderr, flush=True)
+    x = synth.normal_bf16(c.seed, configs.TID_X, (T, H))
+    w = synth.normal_bf16(c.seed, configs.TID_WF, (H,), mean=1.0, std=0.1)
+    DB = hip.DeviceBuffer.from_array
+    sets = [{"x": DB(x), "w": DB(w), "y": hip.DeviceBuffer(T * H * 2)} for _ in range(8)]
+    make = lambda b: [("rms_norm", lambda: q3k.rms_norm(b["x"], b["w"], b["y"], T, H, EPS, stream))]  # noqa: E731
+    ms = time_chain(hip, stream, sets, make, 400, 40)
+    nb = configs.bytes_rms_norm(T, H)
+    out = {"shape": [T, H], "bytes": nb, "us_per_call": round(ms * 1e3, 3), "GB/s": round(nb / (ms * 1e-3) / 1e9, 2)}
+    try:
+        ms_g = time_chain_graph(hip, stream, sets, make, 400, 40)
+        out.update({"us_per_call_graph_replay": round(ms_g * 1e3, 3),
+                    "GB/s_graph_replay": round(nb / (ms_g * 1e-3) / 1e9, 2)})
+    except hip.HipRuntimeError as e:
+        out["graph_error"] = str(e)
+    for st in sets:
+        for b in st.values():
+            b.free()
+    return out
+
+
+def c2_extra(q3k, hip, synth, configs, stream, steps):
+    """Config 2 (Qwen3-0.6B, T = 512 at positions 0..511): the embedding gather (model.cpp:118) from the
+    [151936, 1024] table, residual add + RMSNorm (decoder_layer.cpp:78->88), Q/K norm + RoPE
+    (self_attention.cpp:147-152) and SwiGLU (mlp.cpp:111), as a chain launched op by op and replayed from a HIP
+    graph, and each op alone; GB/s of algorithmic bytes and tokens/s.  Input sets are device copies of one
+    generated set, each with its own token ids, enough of them that one cycle exceeds the Infinity Cache."""
+    c = configs.CONFIGS["c2"]
+    T, H, I = c.tokens, c.hidden, c.inter
+    print("[bench] config 2 chain", file=sys.stderr, flush=True)
+    DB = hip.DeviceBuffer.from_array
+    table = DB(synth.normal_bf16(c.seed, configs.TID_TABLE, (configs.VOCAB, H), std=0.02))
+    base = make_chain_set(hip, synth, configs, c, q3k)
+    for k in ("h2", "d2", "w2", "y2", "qn", "kn"):   # the second residual add + norm is not part of config 2
+        base.pop(k).free()
+    shared = ("w1", "qw", "kw", "cache")
+    per_set = sum(b.nbytes for k, b in base.items() if k not in shared) + T * 4
+    n_sets = max(6, -(-MIN_CYCLE_BYTES // per_set))
+    sets = []
+    for i in range(n_sets):
+        st = base if i == 0 else clone_set(hip, {k: v for k, v in base.items() if k not in shared})
+        st.update({k: base[k] for k in shared})
+        st["ids"] = DB(synth.token_ids(c.seed + i, configs.TID_IDS, (T,), configs.VOCAB))
+        sets.append(st)
+
+    def ops(b):
+        return [
+            ("embedding", lambda: q3k.embedding(b["ids"], T, table, configs.VOCAB, H, b["h1"], stream)),
+            ("add_rms_norm", lambda: q3k.add_rms_norm(b["h1"], b["d1"], b["w1"], b["y1"], T, H, EPS, stream)),
+            ("qk_norm_rope", lambda: q3k.qk_norm_rope(b["q"], b["k"], b["qw"], b["kw"], c.batch, c.seq, c.heads_q,
+                                                      c.heads_kv, D, EPS, b["cache"], c.max_pos, 0, None, stream)),
+            ("silu_mul", lambda: q3k.silu_mul(b["g"], b["u"], b["o"], T * I, stream)),
+        ]
+
+    reps = max(len(sets), steps)
+    ms = time_chain(hip, stream, sets, ops, reps, 4)
+    per_op = time_each_op(hip, stream, sets, ops, reps)
+    op_bytes = {"embedding": configs.bytes_embedding(T, H), "add_rms_norm": configs.bytes_add_rms_norm(T, H),
+                "qk_norm_rope": configs.bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, D, c.distinct_positions()),
+                "silu_mul": configs.bytes_silu_mul(T, I)}
+    chain = configs.c2_chain_bytes(c)
+    assert chain == sum(op_bytes.values())
+    out = {"tokens": T, "chain": "embedding -> add_rms_norm -> qk_norm_rope -> silu_mul", "chain_bytes": chain,
+           "us_per_step": round(ms * 1e3, 2), "GB/s": round(chain / (ms * 1e-3) / 1e9, 1),
+           "pct_of_peak": round(100 * chain / (ms * 1e-3) / 1e9 / PEAK_GBS, 2),
+           "tokens_per_s": round(T / (ms * 1e-3), 1), "input_sets": len(sets),
+           "per_op": {n: {"us": round(t * 1e3, 2), "bytes": op_bytes[n],
+                          "GB/s": round(op_bytes[n] / (t * 1e-3) / 1e9, 1),
+                          "pct_of_peak": round(100 * op_bytes[n] / (t * 1e-3) / 1e9 / PEAK_GBS, 2)}
+                      for n, t in per_op.items()}}
+    try:
+        ms_g = time_chain_graph(hip, stream, sets, ops, reps, 4)
+        out.update({"us_per_step_graph_replay": round(ms_g * 1e3, 2),
+                    "GB/s_graph_replay": round(chain / (ms_g * 1e-3) / 1e9, 1),
+                    "tokens_per_s_graph_replay": round(T / (ms_g * 1e-3), 1)})
+    except hip.HipRuntimeError as e:
+        out["graph_error"] = str(e)
+    seen = set()
+    for st in sets:
+        for b in st.values():
+            if id(b) not in seen:
+                seen.add(id(b))
+                b.free()
+    table.free()
+    return out
+
+
+def ceiling_record(hip, q3k, stream, op_gbs, nbytes, n_in, n_out, in_place, reps, note=None):
+    """An op's measured GB/s beside the ceiling of its own access pattern at its size (pattern_ceiling)."""
+    gbs = pattern_ceiling(hip, q3k, stream, nbytes, n_in, n_out, in_place, reps)
+    rec = {"streams": f"{n_in} in, {n_out} out" + (" (first in place)" if in_place else ""), "bytes_each": nbytes,
+           "GB/s": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2), "op_GB/s": round(op_gbs, 1),
+           "op_frac": round(op_gbs / gbs, 4)}
+    if note:
+        rec["note"] = note
+    return rec
+
+
 def c5_extra(q3k, hip, synth, configs, stream, steps):
     """Config 5 (Qwen3-32B shapes, T = 16384 as 2 x 8192): the fused per-layer chain and each of its ops, plus
     the final RMSNorm [16384, 5120], in GB/s of algorithmic bytes.  Activations are a 64 MiB block of N(0, 1)
@@ -652,7 +766,18 @@ def tp8_shard_extra(q3k, hip, synth, configs, stream, steps):
                 "qk_norm_rope": configs.bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, D, c.distinct_positions()),
                 "silu_mul": configs.bytes_silu_mul(T, I)}
     chain = sum(op_bytes.values())
+    for b in sets[1:]:   # the ceilings below allocate their own buffers
+        for k, v in b.items():
+            if k not in shared:
+                v.free()
+    q_bytes = T * (c.heads_q + c.heads_kv) * D * 2
+    gbs = {n: op_bytes[n] / (t * 1e-3) / 1e9 for n, t in per_op.items()}
+    ceilings = {"add_rms_norm": ceiling_record(hip, q3k, stream, gbs["add_rms_norm"], Ts * H * 2, 2, 2, True, reps),
+                "qk_norm_rope": ceiling_record(hip, q3k, stream, gbs["qk_norm_rope"], q_bytes, 1, 1, True, reps),
+                "silu_mul": ceiling_record(hip, q3k, stream, gbs["silu_mul"], T * I * 2, 2, 1, False, reps)}
+    sets = sets[:1]
     out = {"shapes": {"add_rms_norm": [Ts, H], "q": [T, c.heads_q, D], "k": [T, c.heads_kv, D], "silu_mul": [T, I]},
+           "pattern_ceilings": ceilings,
            "chain_bytes": chain, "chain_ms": round(ms, 5),
            "chain_GB/s": round(chain / (ms * 1e-3) / 1e9, 1),
            "chain_pct_of_peak": round(100 * chain / (ms * 1e-3) / 1e9 / PEAK_GBS, 2),
@@ -756,8 +881,14 @@ def main():
         make_unfused = lambda b: unfused_ops(q3k, c, b, stream)  # noqa: E731
         ms_unfused = time_chain(hip, stream, sets, make_unfused, max(5, args.steps // 2), 3)
         per_unfused = time_each_op(hip, stream, sets, make_unfused, max(5, args.steps // 2), buffers=UNFUSED_BUFFERS)
-        extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5),
-                                   "per_op_ms": {k: round(v, 5) for k, v in per_unfused.items()},
+        unf_bytes = configs.unfused_op_bytes(c)
+        unf_chain = sum(unf_bytes.values())
+        extras["unfused_chain"] = {"ms_per_step": round(ms_unfused, 5), "chain_bytes": unf_chain,
+                                   "GB/s": round(unf_chain / (ms_unfused * 1e-3) / 1e9, 1),
+                                   "per_op": {k: {"ms": round(v, 5), "bytes": unf_bytes[k],
+                                                  "GB/s": round(unf_bytes[k] / (v * 1e-3) / 1e9, 1),
+                                                  "pct_of_peak": round(100 * unf_bytes[k] / (v * 1e-3) / 1e9 / PEAK_GBS, 2)}
+                                              for k, v in per_unfused.items()},
                                    "fused_speedup": round(ms_unfused / ms_step, 3)}
         # copy ceiling: 1 GiB, 128-bit loads and stores
         nb = 1 << 30
@@ -770,15 +901,20 @@ def main():
         # no arithmetic (q3k_bench_stream_u128), back to back over rotating buffers like the per-op figures
         print("[bench] timing access-pattern ceilings", file=sys.stderr, flush=True)
         q_bytes = T * (c.heads_q + c.heads_kv) * D * 2
-        patterns = {"silu_mul": (T * I * 2, 2, 1, False), "add_rms_norm_attn": (T * H * 2, 2, 2, True),
-                    "qk_norm_rope": (q_bytes, 1, 1, True)}
-        ceilings = {}
-        for name, (nb_op, n_in, n_out, in_place) in patterns.items():
-            gbs = pattern_ceiling(hip, q3k, stream, nb_op, n_in, n_out, in_place, args.steps)
-            ceilings[name] = {"streams": f"{n_in} in, {n_out} out" + (" (first in place)" if in_place else ""),
-                              "bytes_each": nb_op, "GB/s": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
-                              "op_frac": round(ops_report[name]["GB/s"] / gbs, 4)}
-        extras["pattern_ceilings"] = ceilings
+        unf = extras["unfused_chain"]["per_op"]
+        patterns = {"silu_mul": (ops_report["silu_mul"]["GB/s"], T * I * 2, 2, 1, False),
+                    "add_rms_norm_attn": (ops_report["add_rms_norm_attn"]["GB/s"], T * H * 2, 2, 2, True),
+                    "qk_norm_rope": (ops_report["qk_norm_rope"]["GB/s"], q_bytes, 1, 1, True),
+                    # the final RMSNorm (model.cpp:146) alone: 64 MB in, 64 MB out
+                    "rms_norm_final": (extras["rms_norm_final"]["GB/s"], T * H * 2, 1, 1, False),
+                    # the drop-in ops of the reference's order (self_attention.cpp:147-152, decoder_layer.cpp:78)
+                    "unfused_rms_norm_q": (unf["rms_norm_q"]["GB/s"], T * c.heads_q * D * 2, 1, 1, False),
+                    "unfused_rms_norm_k": (unf["rms_norm_k"]["GB/s"], T * c.heads_kv * D * 2, 1, 1, False),
+                    "unfused_rope": (unf["rope"]["GB/s"], q_bytes, 1, 1, True),
+                    "unfused_add_inplace": (unf["add_inplace"]["GB/s"], T * H * 2, 2, 1, True)}
+        extras["pattern_ceilings"] = {
+            name: ceiling_record(hip, q3k, stream, gbs, nb_op, n_in, n_out, in_place, args.steps)
+            for name, (gbs, nb_op, n_in, n_out, in_place) in patterns.items()}
         # Q/K norm + RoPE + KV-cache append (self_attention.cpp:147-156) fused, against qk_norm_rope followed by
         # the append; the cache holds the whole sequence (capacity S), written at cached length 0
         print("[bench] timing KV append", file=sys.stderr, flush=True)
@@ -814,6 +950,9 @@ def main():
                                             "unfused_ms": round(ms_kv_pair, 5),
                                             "fused_speedup": round(ms_kv_pair / ms_kv, 3)}
         extras["kv_append"] = {"ms": round(ms_append, 5), "bytes": ab, "GB/s": round(ab / (ms_append * 1e-3) / 1e9, 1)}
+        # K and V in, the two cache layers out (kv_cache.cpp:147-185)
+        extras["pattern_ceilings"]["kv_append"] = ceiling_record(
+            hip, q3k, stream, ab / (ms_append * 1e-3) / 1e9, T * kv_row, 2, 2, False, args.steps)
         for e in kv_sets:
             for buf in e.values():
                 buf.free()
@@ -839,6 +978,10 @@ def main():
                 max(20, len(emb_sets)), 3)
             eb = configs.bytes_embedding(T, H)
             extras["embedding"] = {"ms": round(ms_e, 5), "bytes": eb, "GB/s": round(eb / (ms_e * 1e-3) / 1e9, 1)}
+            # the gathered rows against a contiguous stream of the same bytes in and out
+            extras["pattern_ceilings"]["embedding"] = ceiling_record(
+                hip, q3k, stream, eb / (ms_e * 1e-3) / 1e9, T * H * 2, 1, 1, False, args.steps,
+                note="the op reads T random 8 KB table rows; the ceiling streams the same bytes contiguously")
             # embedding + first input norm fused (model.cpp:118 -> decoder_layer.cpp:72) against the pair
             ms_en = time_chain(hip, stream, emb_sets, lambda e: [
                 ("embedding_rms_norm", lambda: q3k.embedding_rms_norm(e["ids"], T, table, configs.VOCAB, H, w, EPS,
@@ -876,12 +1019,19 @@ def main():
         extras["c3_decode"] = c3_decode_extra(q3k, hip, synth, configs, stream)
         extras["c5_prefill"] = c5_extra(q3k, hip, synth, configs, stream, args.steps)
         extras["tp8_shard"] = tp8_shard_extra(q3k, hip, synth, configs, stream, args.steps)
+        extras["c1_rms_norm"] = c1_extra(q3k, hip, synth, configs, stream)
+        extras["c2_chain"] = c2_extra(q3k, hip, synth, configs, stream, args.steps)
     extras.update(child)
 
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(configs, synth, args.cpu_seconds)
+        if "c1_rms_norm" in extras:   # config 1 on both sides: the reference test's CPU loop against the GPU
+            g = extras["c1_rms_norm"]
+            cpu["c1"]["gpu_us_per_call"] = g["us_per_call"]
+            cpu["c1"]["gpu_speedup_vs_threads"] = round(cpu["c1"]["us_per_call"] / g["us_per_call"], 1)
+            cpu["c1"]["gpu_speedup_vs_1thread"] = round(cpu["c1"]["us_per_call_1thread"] / g["us_per_call"], 1)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

@@ -156,6 +156,19 @@ Q3K_API int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, int3
                   const int32_t *positions, q3k_stream_t stream);
 
 /*
+ * In-place half-split RoPE on q [B, S, Hq * D] and k [B, S, Hkv * D] in one
+ * launch (one grid over the heads of both tensors), with the position rule,
+ * range check and out-of-range behaviour of q3k_rope_bf16; the results equal
+ * q3k_rope_bf16 on q, then on k, bit for bit.  q and k must not overlap.
+ * Replaces both launch_rope calls of qwen3::ops::apply_rope_inplace,
+ * src/ops/rope.cu:305-342 (one launch each for query and key, :326-332).
+ */
+Q3K_API int q3k_rope_qk_bf16(uint16_t *q, uint16_t *k, int64_t B, int64_t S,
+                  int32_t Hq, int32_t Hkv, int32_t D,
+                  const float *cache, int64_t P, int64_t start,
+                  const int32_t *positions, q3k_stream_t stream);
+
+/*
  * Fused per-head Q/K RMSNorm + RoPE, in place, one pass over Q [B, S, Hq*D]
  * and K [B, S, Hkv*D] with weights qw[D], kw[D].  Position rule and the
  * out-of-range behaviour are those of q3k_rope_bf16.

@@ -81,6 +81,7 @@ SIGNATURES = {
     "q3k_add_inplace_bf16": [_p, _p, _i64, _p],
     "q3k_silu_mul_bf16": [_p, _p, _p, _i64, _p],
     "q3k_rope_bf16": [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p, _p],
+    "q3k_rope_qk_bf16": [_p, _p, _i64, _i64, _i32, _i32, _i32, _p, _i64, _i64, _p, _p],
     "q3k_qk_norm_rope_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _p, _i64, _i64, _p, _p],
     "q3k_gqa_attention_bf16": [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _p, _p, _p, _i64, _p],
     "q3k_gqa_attention_workspace_bytes": [_i64, _i64, _i32, _i32, _i32, _i64],
@@ -217,6 +218,11 @@ def silu_mul(g, u, out, n, stream=None):
 
 def rope(x, B, S, heads, D, cache, P, start, positions=None, stream=None):
     _check(load().q3k_rope_bf16(_ptr(x), B, S, heads, D, _ptr(cache), P, start, _ptr(positions), _ptr(stream)))
+
+
+def rope_qk(q, k, B, S, Hq, Hkv, D, cache, P, start, positions=None, stream=None):
+    _check(load().q3k_rope_qk_bf16(_ptr(q), _ptr(k), B, S, Hq, Hkv, D, _ptr(cache), P, start, _ptr(positions),
+                                   _ptr(stream)))
 
 
 def qk_norm_rope(q, k, qw, kw, B, S, Hq, Hkv, D, eps, cache, P, start, positions=None, stream=None):

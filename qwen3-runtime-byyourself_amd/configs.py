@@ -87,6 +87,30 @@ def bytes_silu_mul(T, I):
     return 3 * T * I * 2
 
 
+def bytes_rope(T, Hq, Hkv, D, U):
+    """apply_rope_inplace on Q and K: both read and written once, the table rows of the U positions once."""
+    return 2 * T * (Hq + Hkv) * D * 2 + U * (D // 2) * 2 * 4
+
+
+def unfused_op_bytes(c: Config, U: int | None = None) -> dict:
+    """The reference-order chain's ops (decoder_layer.cpp:78->88, self_attention.cpp:147-152, mlp.cpp:111,
+    :94->:72), each byte counted once per op."""
+    T, H = c.tokens, c.hidden
+    U = c.distinct_positions() if U is None else U
+    return {"add_inplace": bytes_add_inplace(T, H), "rms_norm": bytes_rms_norm(T, H),
+            "rms_norm_q": bytes_rms_norm(T * c.heads_q, HEAD_DIM), "rms_norm_k": bytes_rms_norm(T * c.heads_kv, HEAD_DIM),
+            "rope": bytes_rope(T, c.heads_q, c.heads_kv, HEAD_DIM, U), "add_inplace_2": bytes_add_inplace(T, H),
+            "rms_norm_2": bytes_rms_norm(T, H), "silu_mul": bytes_silu_mul(T, c.inter)}
+
+
+def c2_chain_bytes(c: Config) -> int:
+    """Benchmark config 2's chain: embedding gather, residual add + RMSNorm, Q/K norm + RoPE, SwiGLU."""
+    T = c.tokens
+    return (bytes_embedding(T, c.hidden) + bytes_add_rms_norm(T, c.hidden)
+            + bytes_qk_norm_rope(T, c.heads_q, c.heads_kv, HEAD_DIM, c.distinct_positions())
+            + bytes_silu_mul(T, c.inter))
+
+
 def chain_bytes(c: Config, U: int | None = None) -> int:
     """Per-layer non-GEMM chain, fused: 2 x add_rms_norm + qk_norm_rope + silu_mul."""
     T = c.tokens

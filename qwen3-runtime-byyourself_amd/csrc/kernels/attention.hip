@@ -42,6 +42,7 @@
 // structure with wave reductions.
 #include <type_traits>
 
+#include "dispatch.hpp"
 #include "q3k_common.hpp"
 
 namespace q3k
@@ -55,14 +56,14 @@ namespace q3k
         typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
         typedef __attribute__((address_space(3))) void lds_void_t;
 
-        constexpr int kAttD = 128;
-        constexpr int kKeyTile = 64;                          // keys per pipeline step
+        constexpr int kAttD = kAttHeadDim;
+        constexpr int kKeyTile = kAttKeyTile;                 // keys per pipeline step
         constexpr int kRowBytes = kAttD * 2;                  // one K or V row in LDS
         constexpr int kHalfBytes = kKeyTile * kRowBytes;      // the K (or V) rows of a tile
         constexpr int kRowsPerLoad = kWave * 16 / kRowBytes;  // rows one wave-wide 16-byte load fills
         constexpr int kAhead = 2;                             // LDS fragment reads in flight ahead of use
         constexpr float kLazyMax = 8.0f;                      // log2 headroom before the softmax reference moves
-        constexpr int kAttWaves = 4;                          // waves per matrix-core block
+        constexpr int kAttWaves = kAttWavesPerBlock;          // waves per matrix-core block
         constexpr int kAttBlock = kAttWaves * kWave;
         constexpr float kLog2e = 1.4426950408889634f;
 
@@ -578,7 +579,7 @@ namespace q3k
         // 2^(m_s - max m) (the maxima are in the log2 domain), then
         // sum_s w_s O_s / sum_s w_s l_s; lane t holds dims 2t, 2t + 1, and the
         // four waves' partial sums meet in LDS.
-        constexpr int kMaxSplits = 64;
+        constexpr int kMaxSplits = kAttMaxSplits;
         constexpr int kCombineWaves = 4;
         constexpr int kSplitsPerWave = kMaxSplits / kCombineWaves;
 
@@ -696,72 +697,15 @@ namespace q3k
             }
         }
 
-        bool mfma_ok(const AttnArgs &a, int32_t G)
-        {
-            const bool g_ok = G >= 1 && G <= 32;
-            // tile loads use 32-bit byte offsets of up to kKeyTile rows
-            const int64_t row_limit = (INT32_MAX - kRowBytes) / (2 * kKeyTile);
-            return g_ok && a.D == kAttD && a.start + a.S <= INT32_MAX && a.ks1 <= row_limit && a.vs1 <= row_limit &&
-                   a.ks3 == 1 && a.vs3 == 1 && a.ks0 % 8 == 0 && a.ks1 % 8 == 0 &&
-                   a.ks2 % 8 == 0 && a.vs0 % 8 == 0 && a.vs1 % 8 == 0 && a.vs2 % 8 == 0 && aligned16(a.q) &&
-                   aligned16(a.k) && aligned16(a.v) && aligned_to(a.out, 8);
-        }
-
-        // Below this many blocks the grid leaves CUs idle and the key range is
-        // split; a slice keeps at least two tiles, or one for a decode step
-        // (one query position), whose slices of up to two tiles run as
-        // one-wave blocks: the four-wave block computes one position in one
-        // wave, so each slice then takes a wave of its own instead of a block
-        // (B 1 x 4096 keys: 8.7 against 10.3 us; from B 4 the four-wave
-        // blocks, which share each tile's loads, are as fast or faster).
-        constexpr int64_t kSplitTargetBlocks = 512;
-        constexpr int32_t kMinSplitKeys = 2 * kKeyTile;
-        constexpr int32_t kMinDecodeSplitKeys = kKeyTile;
-        constexpr int32_t kMaxOneWaveSplitKeys = 2 * kKeyTile;
-
-        struct SplitPlan
-        {
-            int32_t splits = 1;
-            int32_t split_keys = INT32_MAX;
-            int64_t bytes = 0;
-        };
-
-        SplitPlan plan_split(int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int64_t cached)
-        {
-            SplitPlan p;
-            const int32_t G = Hq / Hkv;
-            const int64_t cols = S * G, block_cols = 32 * kAttWaves;
-            const int64_t blocks = B * Hkv * ((cols + block_cols - 1) / block_cols);
-            const int32_t min_keys = S == 1 ? kMinDecodeSplitKeys : kMinSplitKeys;
-            if (blocks >= kSplitTargetBlocks || cached < 2 * min_keys)
-                return p;
-            int64_t want = (kSplitTargetBlocks + blocks - 1) / blocks;
-            const int64_t most = cached / min_keys;
-            if (want > most)
-                want = most;
-            if (want > kMaxSplits)
-                want = kMaxSplits;
-            if (want < 2)
-                return p;
-            int64_t keys = (cached + want - 1) / want;
-            keys = (keys + kKeyTile - 1) / kKeyTile * kKeyTile;
-            p.splits = static_cast<int32_t>((cached + keys - 1) / keys);
-            p.split_keys = static_cast<int32_t>(keys);
-            if (p.splits < 2)
-                return SplitPlan{};
-            p.bytes = static_cast<int64_t>(p.splits) * B * S * Hq * (kAttD + 2) * 4;
-            return p;
-        }
-
         template <int G>
-        int launch_mfma(AttnArgs a, int64_t B, hipStream_t stream)
+        int launch_mfma(AttnArgs a, int64_t B, int waves, hipStream_t stream)
         {
             const int64_t cols = a.S * (a.Hq / a.Hkv), block_cols = 32 * kAttWaves;
             a.qblocks = static_cast<int32_t>((cols + block_cols - 1) / block_cols);
             const int64_t blocks = B * a.Hkv * a.qblocks * a.splits;
             if (!launch_fits(blocks, kAttBlock) || (a.splits > 1 && !launch_fits(a.rows, kCombineWaves * kWave)))
                 return set_error(Q3K_ERR_OVERFLOW, "GQA grid is too large");
-            if (a.splits > 1 && a.S == 1 && a.split_keys <= kMaxOneWaveSplitKeys)
+            if (waves == 1)
             {
                 // one query position (at most 32 columns) per block either way, so the grid is the same
                 static_assert(G == 0 || 32 / G >= 1, "one position per wave at least");
@@ -835,27 +779,28 @@ extern "C" int q3k_gqa_attention_bf16(const uint16_t *q, const uint16_t *k_cache
                nullptr,
                nullptr,
                B * S * Hq};
-    const int32_t G = Hq / Hkv;
-    if (mfma_ok(a, G))
+    const AttnPlan plan =
+        plan_attention(B, S, Hq, Hkv, D, start, k_strides, v_strides,
+                       aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned_to(out, 8),
+                       workspace_bytes, workspace != nullptr && aligned16(workspace));
+    if (plan.mfma)
     {
-        const SplitPlan plan = plan_split(B, S, Hq, Hkv, cached);
-        if (plan.splits > 1 && plan.splits <= kMaxSplits && workspace != nullptr && workspace_bytes >= plan.bytes &&
-            aligned16(workspace))
+        if (plan.split.splits > 1)
         {
-            a.splits = plan.splits;
-            a.split_keys = plan.split_keys;
+            a.splits = plan.split.splits;
+            a.split_keys = plan.split.split_keys;
             a.part_o = static_cast<float *>(workspace);
-            a.part_ml = a.part_o + static_cast<int64_t>(plan.splits) * a.rows * kAttD;
+            a.part_ml = a.part_o + static_cast<int64_t>(plan.split.splits) * a.rows * kAttD;
         }
-        switch (G)
+        switch (plan.g_instance)
         {
-        case 1: return launch_mfma<1>(a, B, s);
-        case 2: return launch_mfma<2>(a, B, s);
-        case 4: return launch_mfma<4>(a, B, s);
-        case 8: return launch_mfma<8>(a, B, s);
-        case 16: return launch_mfma<16>(a, B, s);
-        case 32: return launch_mfma<32>(a, B, s);
-        default: return launch_mfma<0>(a, B, s);
+        case 1: return launch_mfma<1>(a, B, plan.waves, s);
+        case 2: return launch_mfma<2>(a, B, plan.waves, s);
+        case 4: return launch_mfma<4>(a, B, plan.waves, s);
+        case 8: return launch_mfma<8>(a, B, plan.waves, s);
+        case 16: return launch_mfma<16>(a, B, plan.waves, s);
+        case 32: return launch_mfma<32>(a, B, plan.waves, s);
+        default: return launch_mfma<0>(a, B, plan.waves, s);
         }
     }
     const int64_t rows = B * S * Hq;
@@ -872,5 +817,5 @@ extern "C" int64_t q3k_gqa_attention_workspace_bytes(int64_t B, int64_t S, int32
     if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != q3k::kAttD || cached < S ||
         B * S * Hq > INT32_MAX)
         return 0;
-    return q3k::plan_split(B, S, Hq, Hkv, cached).bytes;
+    return q3k::plan_attention_split(B, S, Hq, Hkv, cached).bytes;
 }

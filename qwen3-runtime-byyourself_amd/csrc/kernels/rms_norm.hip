@@ -137,38 +137,87 @@ namespace q3k
                     wv[i] = wvec[first_vec + i * vec_step];
         }
 
-        // Group of G lanes per row (G <= 64), VPT vectors per lane.
-        template <int G, int VPT, int MODE, int NTM, bool FULL>
+        // Group of G lanes per row (G <= 64), VPT vectors per lane, RPG rows
+        // per lane group.  The rows of a wave are contiguous: lane group j of
+        // wave w takes rows w * (64 / G) * RPG + j + (64 / G) * r, r < RPG, so
+        // each load instruction covers 64 / G whole rows.  Every x load (of
+        // all RPG rows) is issued first, then d, then the weights once.
+        template <int G, int VPT, int RPG, int MODE, int NTM, bool FULL>
         __global__ __launch_bounds__(kBlock) void rms_rows_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
             int64_t rows, int nvec, float inv_n, float eps, RowMap map)
         {
-            constexpr int kRowsPerBlock = kBlock / G;
+            constexpr int kGroups = kWave / G;
             const int lane = threadIdx.x % G;
-            const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
-            if (row >= rows)
+            const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+            const int64_t row0 = wave * kGroups * RPG + (threadIdx.x % kWave) / G;
+            if (row0 >= rows)
                 return;
-
-            Vec8 x[VPT], dv[VPT], wv[VPT];
-            bool live[VPT];
-            load_row<VPT, MODE, NTM, FULL>(row_source<MODE>(h, map, row, nvec), d, map, row, nvec,
-                                           reinterpret_cast<const Vec8 *>(w), lane, G, x, dv, wv, live);
-            const float partial = add_and_square<VPT, MODE>(x, dv, live);
-            if constexpr (MODE != kNorm)
+            const Vec8 zero = {{0u, 0u, 0u, 0u}};
+            Vec8 x[RPG][VPT], dv[RPG][VPT], wv[VPT];
+            bool live[RPG][VPT];
+            const Vec8 *src[RPG];
+#pragma unroll
+            for (int r = 0; r < RPG; ++r)
             {
-                Vec8 *hrow = residual_row<MODE>(h, map, row, nvec);
+                const int64_t row = row0 + kGroups * r;
+                src[r] = row < rows ? row_source<MODE>(h, map, row, nvec) : nullptr;
 #pragma unroll
                 for (int i = 0; i < VPT; ++i)
-                    if (live[i])
-                        store8<nt_store(NTM)>(hrow + lane + i * G, x[i]);
+                    live[r][i] = row < rows && (FULL || lane + i * G < nvec);
             }
-            const float inv = inverse_rms(group_sum<G>(partial), inv_n, eps);
-            Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * nvec;
+#pragma unroll
+            for (int r = 0; r < RPG; ++r)
+#pragma unroll
+                for (int i = 0; i < VPT; ++i)
+                {
+                    if (!live[r][i])
+                        continue;
+                    if constexpr (MODE == kGatherNorm)
+                        x[r][i] = src[r] != nullptr ? load8<false>(src[r] + lane + i * G) : zero;
+                    else
+                        x[r][i] = load8<nt_load(NTM)>(src[r] + lane + i * G);
+                }
+            if constexpr (MODE == kAddNorm)
+            {
+#pragma unroll
+                for (int r = 0; r < RPG; ++r)
+                {
+                    const Vec8 *drow =
+                        reinterpret_cast<const Vec8 *>(d) + (map.first + (row0 + kGroups * r) * map.stride) * nvec;
+#pragma unroll
+                    for (int i = 0; i < VPT; ++i)
+                        if (live[r][i])
+                            dv[r][i] = load8<nt_load(NTM)>(drow + lane + i * G);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < VPT; ++i)
-                if (live[i])
-                    store8<nt_store(NTM)>(yrow + lane + i * G, norm_scale8(x[i], wv[i], inv));
+                if (FULL || lane + i * G < nvec)
+                    wv[i] = reinterpret_cast<const Vec8 *>(w)[lane + i * G];
+#pragma unroll
+            for (int r = 0; r < RPG; ++r)
+            {
+                const int64_t row = row0 + kGroups * r;
+                if (row >= rows)
+                    continue;
+                const float partial = add_and_square<VPT, MODE>(x[r], dv[r], live[r]);
+                if constexpr (MODE != kNorm)
+                {
+                    Vec8 *hrow = residual_row<MODE>(h, map, row, nvec);
+#pragma unroll
+                    for (int i = 0; i < VPT; ++i)
+                        if (live[r][i])
+                            store8<nt_store(NTM)>(hrow + lane + i * G, x[r][i]);
+                }
+                const float inv = inverse_rms(group_sum<G>(partial), inv_n, eps);
+                Vec8 *yrow = reinterpret_cast<Vec8 *>(y) + row * nvec;
+#pragma unroll
+                for (int i = 0; i < VPT; ++i)
+                    if (live[r][i])
+                        store8<nt_store(NTM)>(yrow + lane + i * G, norm_scale8(x[r][i], wv[i], inv));
+            }
         }
 
         // One row per block of WPR waves, VPT vectors per lane; the wave sums
@@ -296,13 +345,14 @@ namespace q3k
 
         // Non-temporal mode bits (loads | stores), measured on MI355X with
         // input cycles far above the Infinity Cache: non-temporal loads and
-        // stores for every row width, except narrow rows without the fused
-        // add, where plain loads are faster.  Gathered rows use plain loads
-        // (random rows, as in the embedding kernel).
+        // stores for every row width (128-wide rows, 262144 of them: 75.5%
+        // of peak against 73.7% with plain loads; 1024-wide, 65536 rows:
+        // 78.2% against 75.3%).  Gathered rows use plain loads (random rows,
+        // as in the embedding kernel).
         template <int MODE>
         constexpr int ntm_block() { return MODE == kGatherNorm ? 2 : 3; }
         template <int MODE>
-        constexpr int ntm_rows() { return MODE == kNorm ? 2 : MODE == kAddNorm ? 3 : 2; }
+        constexpr int ntm_rows() { return MODE == kGatherNorm ? 2 : 3; }
         // Wave priority while the loads are issued: raised priority helped the
         // fused add while stores were written back from L2 at the end of each
         // kernel; with write-through stores the default is faster (77.7%
@@ -325,20 +375,43 @@ namespace q3k
             hipStream_t stream;
         };
 
-        template <int G, int VPT, int MODE>
-        bool launch_rows(const Launch &l)
+        template <int G, int VPT, int RPG, int MODE>
+        bool launch_rows_rpg(const Launch &l)
         {
-            constexpr int kRowsPerBlock = kBlock / G;
+            constexpr int kRowsPerBlock = kBlock / G * RPG;
             if (!rms_rows_fit(l.rows, G))
                 return false;
             const dim3 grid(static_cast<unsigned>(blocks_for(l.rows, kRowsPerBlock)));
             if (l.nvec == G * VPT)
-                rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), true><<<grid, dim3(kBlock), 0, l.stream>>>(
+                rms_rows_kernel<G, VPT, RPG, MODE, ntm_rows<MODE>(), true><<<grid, dim3(kBlock), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
             else
-                rms_rows_kernel<G, VPT, MODE, ntm_rows<MODE>(), false><<<grid, dim3(kBlock), 0, l.stream>>>(
+                rms_rows_kernel<G, VPT, RPG, MODE, ntm_rows<MODE>(), false><<<grid, dim3(kBlock), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
             return true;
+        }
+
+        // Rows per lane group of the plain norm (measured on MI355X, nt loads,
+        // rotations past the Infinity Cache): 128-wide rows (the per-head Q/K
+        // norms) take four rows per 16-lane group for 16384 .. 65536 rows (the
+        // K norm of config 4, 65536 rows: 6.4 against 7.4 us with one) and one
+        // beyond (262144 rows: 22.2 against 23.2 us with four); 1024-wide rows
+        // take two per wave from 4096 rows (8192 rows: 6.4 against 7.4 us; 65536
+        // rows: equal).  Fewer rows (decode) keep one, for more waves.
+        template <int G, int VPT, int MODE>
+        bool launch_rows(const Launch &l)
+        {
+            if constexpr (MODE == kNorm && G == 16 && VPT == 1)
+            {
+                if (l.rows >= 16384 && l.rows <= 65536)
+                    return launch_rows_rpg<G, VPT, 4, MODE>(l);
+            }
+            if constexpr (MODE == kNorm && G == 64 && VPT == 2)
+            {
+                if (l.rows >= 4096)
+                    return launch_rows_rpg<G, VPT, 2, MODE>(l);
+            }
+            return launch_rows_rpg<G, VPT, 1, MODE>(l);
         }
 
         template <int WPR, int VPT, int MODE>

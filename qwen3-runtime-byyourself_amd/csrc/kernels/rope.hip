@@ -17,6 +17,7 @@
 // Arithmetic follows src/ops/rope.cu:64-84: c, s from the fp32 table,
 // x1' = RNE(x1*c - x2*s), x2' = RNE(x2*c + x1*s), products and sum each
 // rounded to fp32 (no contraction).
+#include "dispatch.hpp"
 #include "q3k_common.hpp"
 
 namespace q3k
@@ -349,11 +350,6 @@ namespace q3k
             }
         }
 
-        bool fast_ok(const void *x, const float *cache, int32_t heads, int32_t head_dim)
-        {
-            return head_dim == kHeadDim && aligned16(x) && aligned16(cache);
-        }
-
         void launch_generic_rope(uint16_t *x, int32_t heads, int32_t head_dim, const RopeShape &rs, hipStream_t stream)
         {
             const int64_t pairs = rs.tokens * heads * (head_dim / 2);
@@ -397,55 +393,36 @@ namespace q3k
             return Q3K_OK;
         }
 
-        // waves over the tensor's rows: whole when heads % (4 hg) == 0, the last
-        // one partial otherwise (ANYH, hg = 1)
-        int64_t waves_for(int64_t tokens, int32_t heads, int hg)
-        {
-            return (tokens * heads + kHeadsPerWave * hg - 1) / (kHeadsPerWave * hg);
-        }
-        bool any_heads(int32_t hq, int32_t hk) { return hq % kHeadsPerWave != 0 || hk % kHeadsPerWave != 0; }
-
-        // Heads per lane: 4 when the head count allows it (32 or 64 query
-        // heads), else 2 (8 KV heads), else 1.
-        int heads_per_lane(int32_t heads) { return heads % 16 == 0 ? 4 : heads % 8 == 0 ? 2 : 1; }
-        constexpr int64_t kSmallLaunchHeads = 16384; // below this many (token, head) rows: one head per lane group
-
         template <bool NORM, bool KV, int HGQ, int HGK, int ANYH = 0>
         void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
                              int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv, hipStream_t stream)
         {
             constexpr int NTM = NORM ? kNtmNormRope : kNtmRope;
-            const int64_t q_waves = waves_for(tokens, hq, HGQ);
-            const int64_t total = q_waves + (k == nullptr ? 0 : waves_for(tokens, hk, HGK));
+            const int64_t q_waves = rope_waves(tokens, hq, HGQ);
+            const int64_t total = q_waves + (k == nullptr ? 0 : rope_waves(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
             rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
                 <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
+        // The instance the plan (plan_rope) names: heads per lane of Q and K, or
+        // rows per lane group for head counts that are not a multiple of 4.
         template <bool NORM, bool KV = false>
-        void launch_heads(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
-                          int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream, const KvDest &kv = {})
+        void launch_heads(const RopePlan &plan, uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw,
+                          int32_t hq, int32_t hk, int64_t tokens, const RopeShape &rs, float eps, hipStream_t stream,
+                          const KvDest &kv = {})
         {
-            // A small launch (decode: a few tokens) spreads one head per lane
-            // group over more waves: fewer heads per wave shorten its serial
-            // chain, and the waves fill more CUs.
-            if (any_heads(hq, k == nullptr ? 0 : hk))
+            if (plan.any_heads != 0)
             {
-                // per-lane rows only for the tensor whose head count needs them
-                const int any = (hq % kHeadsPerWave != 0 ? 1 : 0) | (k != nullptr && hk % kHeadsPerWave != 0 ? 2 : 0);
-                if (any == 1)
+                if (plan.any_heads == 1)
                     launch_heads_hg<NORM, KV, 1, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
-                else if (any == 2)
+                else if (plan.any_heads == 2)
                     launch_heads_hg<NORM, KV, 1, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 else
                     launch_heads_hg<NORM, KV, 1, 1, 3>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 return;
             }
-            const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kSmallLaunchHeads;
-            const int gq = small ? 1 : heads_per_lane(hq);
-            const int gk = small ? 1 : (k == nullptr ? gq : heads_per_lane(hk));
-            const int key = gq * 10 + gk;
-            switch (key)
+            switch (plan.hg_q * 10 + plan.hg_k)
             {
             case 44: launch_heads_hg<NORM, KV, 4, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
             case 42: launch_heads_hg<NORM, KV, 4, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
@@ -457,17 +434,6 @@ namespace q3k
             case 12: launch_heads_hg<NORM, KV, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
             default: launch_heads_hg<NORM, KV, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
             }
-        }
-
-        // every tensor's rows below 2^31, and the grid of the waves the launcher
-        // makes (each tensor's last wave may be partial) within the launch limit
-        bool grid_ok(int64_t tokens, int32_t hq, int32_t hk)
-        {
-            if (!rope_heads_fit(tokens, hq) || (hk > 0 && !rope_heads_fit(tokens, hk)) ||
-                !rope_heads_fit(tokens, hq + hk))
-                return false;
-            const int64_t waves = waves_for(tokens, hq, 1) + waves_for(tokens, hk, 1);
-            return launch_fits(blocks_for(waves, kWavesPerBlock), kBlock);
         }
     } // namespace
 } // namespace q3k
@@ -484,11 +450,38 @@ extern "C" int q3k_rope_bf16(uint16_t *x, int64_t B, int64_t S, int32_t heads, i
         return Q3K_OK;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    if (fast_ok(x, cache, heads, D) && grid_ok(tokens, heads, 0))
-        launch_heads<false>(x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, s);
+    const RopePlan plan = plan_rope(tokens, heads, 0, D, aligned16(x) && aligned16(cache));
+    if (plan.fast)
+        launch_heads<false>(plan, x, nullptr, nullptr, nullptr, heads, 0, tokens, rs, 0.0f, s);
     else
         launch_generic_rope(x, heads, D, rs, s);
     return check_launch("apply_rope");
+}
+
+extern "C" int q3k_rope_qk_bf16(uint16_t *q, uint16_t *k, int64_t B, int64_t S, int32_t Hq, int32_t Hkv, int32_t D,
+                                const float *cache, int64_t P, int64_t start, const int32_t *positions,
+                                q3k_stream_t stream)
+{
+    using namespace q3k;
+    if (const int st = validate_rope(q, B, S, Hq, D, cache, P, start, positions))
+        return st;
+    if (const int st = validate_rope(k, B, S, Hkv, D, cache, P, start, positions))
+        return st;
+    const int64_t tokens = B * S;
+    if (tokens == 0)
+        return Q3K_OK;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const RopeShape rs{tokens, S, P, start, positions, cache};
+    const RopePlan plan = plan_rope(tokens, Hq, Hkv, D, aligned16(q) && aligned16(k) && aligned16(cache));
+    if (plan.fast)
+    {
+        // one grid: the waves before q_waves rotate Q, the rest K
+        launch_heads<false>(plan, q, k, nullptr, nullptr, Hq, Hkv, tokens, rs, 0.0f, s);
+        return check_launch("apply_rope");
+    }
+    launch_generic_rope(q, Hq, D, rs, s);
+    launch_generic_rope(k, Hkv, D, rs, s);
+    return check_launch("apply_rope (generic)");
 }
 
 extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw,
@@ -512,10 +505,11 @@ extern "C" int q3k_qk_norm_rope_bf16(uint16_t *q, uint16_t *k, const uint16_t *q
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "Q/K norm weights must be 2-byte aligned");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) &&
-        grid_ok(tokens, Hq, Hkv))
+    const RopePlan plan =
+        plan_rope(tokens, Hq, Hkv, D, aligned16(q) && aligned16(k) && aligned16(cache) && aligned16(qw) && aligned16(kw));
+    if (plan.fast)
     {
-        launch_heads<true>(q, k, qw, kw, Hq, Hkv, tokens, rs, eps, s);
+        launch_heads<true>(plan, q, k, qw, kw, Hq, Hkv, tokens, rs, eps, s);
         return check_launch("qk_norm_rope");
     }
     // Unfused fallback: per-head RMSNorm in place, then RoPE.
@@ -556,11 +550,13 @@ extern "C" int q3k_qk_norm_rope_kv_append_bf16(uint16_t *q, const uint16_t *k, c
         return set_error(Q3K_ERR_INVALID_ARGUMENT, "bf16 pointers must be 2-byte aligned");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const RopeShape rs{tokens, S, P, start, positions, cache};
-    if (fast_ok(q, cache, Hq, D) && fast_ok(k, cache, Hkv, D) && aligned16(qw) && aligned16(kw) && aligned16(v) &&
-        aligned16(k_cache) && aligned16(v_cache) && grid_ok(tokens, Hq, Hkv))
+    const RopePlan plan = plan_rope(tokens, Hq, Hkv, D,
+                                    aligned16(q) && aligned16(k) && aligned16(cache) && aligned16(qw) && aligned16(kw) &&
+                                        aligned16(v) && aligned16(k_cache) && aligned16(v_cache));
+    if (plan.fast)
     {
         const KvDest kv{v, k_cache, v_cache, seq_cap, cache_start};
-        launch_heads<true, true>(q, const_cast<uint16_t *>(k), qw, kw, Hq, Hkv, tokens, rs, eps, s, kv);
+        launch_heads<true, true>(plan, q, const_cast<uint16_t *>(k), qw, kw, Hq, Hkv, tokens, rs, eps, s, kv);
         return check_launch("qk_norm_rope_kv_append");
     }
     // Generic path: copy K and V into the cache, then norm and rotate the

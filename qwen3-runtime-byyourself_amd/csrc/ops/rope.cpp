@@ -90,11 +90,11 @@ namespace qwen3::ops
             const auto D = static_cast<std::int32_t>(cache.shape()[1] * 2);
             const auto *table = static_cast<const float *>(cache.data());
             const std::int64_t P = cache.shape()[0];
+            // query and key in one launch (the reference makes one per tensor,
+            // src/ops/rope.cu:326-332); the results are the same bits
             detail::launch_on(query.device(), [&](q3k_stream_t stream) {
-                int st = q3k_rope_bf16(detail::bf16_ptr(query), B, S, hq, D, table, P, start, positions, stream);
-                if (st == Q3K_OK)
-                    st = q3k_rope_bf16(detail::bf16_ptr(key), B, S, hkv, D, table, P, start, positions, stream);
-                return st;
+                return q3k_rope_qk_bf16(detail::bf16_ptr(query), detail::bf16_ptr(key), B, S, hq, hkv, D, table, P,
+                                        start, positions, stream);
             });
         }
 

@@ -68,6 +68,11 @@ def check_exact(name, got, want):
                              f"got 0x{int(got[i]):04x} want 0x{int(want[i]):04x}")
 
 
+def record(stats):
+    """Add a comparison made elsewhere (a C++ test's PARITY line) to the report."""
+    _REPORT.append(stats)
+
+
 def write_report():
     path = os.environ.get("Q3K_PARITY_REPORT")
     if path and _REPORT:

@@ -1,7 +1,9 @@
-"""Fallback guards: the head layouts of the Qwen3 family and of their tensor-parallel shards must run on the fast
-kernels, not on the generic ones.  The generic kernels give the same results (the parity tests cover both), so
-only time tells them apart: at these sizes the generic Q/K path ran 8x and the generic attention ~165x slower than
-the fast ones.  The floors sit far below the fast kernels (3-6x) and far above the generic ones."""
+"""Fallback guards, second line: the head layouts of the Qwen3 family and of their tensor-parallel shards must run
+on the fast kernels, not on the generic ones.  The launchers' decisions themselves are checked on the host,
+deterministically, by tests/cpp/dispatch_cpu_test.cpp (csrc/kernels/dispatch.hpp is the only place they are made).
+This file checks the same on the device through time: the generic kernels give the same results (the parity tests
+cover both), but at these sizes the generic Q/K path ran 8x and the generic attention ~165x slower than the fast
+ones.  The floors sit far below the fast kernels (3-6x) and far above the generic ones."""
 import numpy as np
 import pytest
 
