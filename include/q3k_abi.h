@@ -249,7 +249,9 @@ Q3K_API int64_t q3k_argmax_workspace_bytes(int64_t rows, int64_t search_size);
  * workspace.  Every input fits it (slicing needs fewer than 8 KiB); a plan
  * needing more returns Q3K_ERR_INVALID_ARGUMENT.  The call itself allocates
  * nothing.  Calls on one GPU share that array, so calls that overlap on one
- * GPU race.  No counterpart in the reference.
+ * GPU race.  The first call on each GPU looks up the array's device address
+ * (a host-side query under a lock); make that call before capturing the
+ * entry point into a HIP graph.  No counterpart in the reference.
  */
 Q3K_API int q3k_argmax_bf16_noalloc(const uint16_t *x, int32_t *out, int64_t rows,
                   int64_t row_stride, int64_t search_size,

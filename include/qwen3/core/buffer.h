@@ -3,7 +3,11 @@
 // Owning, move-only byte storage on the host (64-byte aligned) or on a GPU
 // (hipMalloc; device blocks of at most 4 MiB are kept for reuse when their
 // Buffer is destroyed, in the order of the default stream, up to 64 MiB per
-// device).  Contract pinned by the reference's tests/unit/buffer_cpu_test.cpp
+// device).  Unlike hipFree, keeping a block does not wait for the device:
+// work on a stream other than the default one that uses a small tensor must
+// have finished before the tensor is destroyed.  QWEN3_DEVICE_BLOCK_CACHE=0
+// in the environment turns the cache off (every block freed with hipFree, as
+// the reference's Buffer does).  Contract pinned by the reference's tests/unit/buffer_cpu_test.cpp
 // and buffer_cuda_test.cpp: zero bytes give a null pointer, a moved-from
 // buffer is empty, copies check sizes (std::invalid_argument) and ranges
 // (std::out_of_range), GPU allocation failures throw std::runtime_error and

@@ -10,6 +10,7 @@
 #include <mutex>
 #include <new>
 #include <stdexcept>
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -28,6 +29,19 @@ namespace qwen3
 
         std::atomic<std::uint64_t> g_device_allocations{0};
         thread_local int t_fresh_blocks = 0;  // FreshDeviceBlocks scopes open on this thread
+
+        // QWEN3_DEVICE_BLOCK_CACHE=0 in the environment turns the small-block
+        // cache off for the process: every device block is then freed with
+        // hipFree, which waits for the whole device, as the reference's
+        // Buffer does.  Read once, at the first device allocation.
+        bool block_cache_enabled()
+        {
+            static const bool enabled = [] {
+                const char *v = std::getenv("QWEN3_DEVICE_BLOCK_CACHE");
+                return v == nullptr || std::string(v) != "0";
+            }();
+            return enabled;
+        }
 
         // Small device blocks are kept when their Buffer is destroyed and
         // handed to the next Buffer of the same size class on that device,
@@ -119,7 +133,7 @@ namespace qwen3
 
         void *allocate_device(std::size_t bytes, int index)
         {
-            const bool small = SmallBlockCache::cached(bytes);
+            const bool small = SmallBlockCache::cached(bytes) && block_cache_enabled();
             const std::size_t alloc = small ? SmallBlockCache::size_class(bytes) : bytes;
             if (small && t_fresh_blocks == 0)
                 if (void *p = block_cache().take(index, alloc))
@@ -136,7 +150,8 @@ namespace qwen3
         {
             try
             {
-                if (SmallBlockCache::cached(bytes) && block_cache().keep(index, SmallBlockCache::size_class(bytes), p))
+                if (SmallBlockCache::cached(bytes) && block_cache_enabled() &&
+                    block_cache().keep(index, SmallBlockCache::size_class(bytes), p))
                     return;
             }
             catch (...)

@@ -38,7 +38,14 @@ namespace qwen3::io_detail
             std::uint64_t value = 0;   // valid when is_unsigned
         };
 
-        explicit JsonCursor(std::string_view text) : text_(text) {}
+        // A leading UTF-8 byte order mark (EF BB BF) is skipped, as nlohmann's
+        // lexer does for every document the reference parses.
+        explicit JsonCursor(std::string_view text) : text_(text)
+        {
+            if (text_.size() >= 3 && static_cast<unsigned char>(text_[0]) == 0xEF &&
+                static_cast<unsigned char>(text_[1]) == 0xBB && static_cast<unsigned char>(text_[2]) == 0xBF)
+                at_ = 3;
+        }
 
         // Kind of the next value (whitespace skipped); throws at end of input
         // or on a character that cannot start a value.

@@ -144,7 +144,9 @@ namespace qwen3
                         }
                     }
                 }
-                cur.finish();
+                // nothing after the root value is read: the reference reads the
+                // index with nlohmann's stream operator, which stops at the end
+                // of the first value (safetensors_checkpoint.cpp:36)
             }
             catch (const std::runtime_error &e)
             {
@@ -198,7 +200,7 @@ namespace qwen3
         if (has_single && has_index)
             fail("model directory contains both model.safetensors and model.safetensors.index.json");
         if (!has_single && !has_index)
-            fail("model directory contains neither model.safetensors nor model.safetensors.index.json");
+            fail("model directory contains neither model.safetensors ans model.safetensor.index.json");
 
         if (has_single)
         {
@@ -227,7 +229,7 @@ namespace qwen3
         for (const auto &[tensor, shard] : idx.weight_map)
         {
             if (tensor.empty() || !shard)
-                fail("checkpoint weight_map contains an invalid entry");
+                fail("checkpoint weight_map contains an valid entry");
             auto found = shard_of_name.find(*shard);
             if (found == shard_of_name.end())
             {
@@ -283,7 +285,7 @@ namespace qwen3
         if (!missing.empty())
             fail("indexed tensor is missing from its shard: " + *std::min_element(missing.begin(), missing.end()));
         if (bytes != *idx.total_size)
-            fail("checkpoint total_size mismatch: expected " + std::to_string(*idx.total_size) + ", got " +
+            fail("checkpoint total_size mismatch: expected" + std::to_string(*idx.total_size) + ", got" +
                  std::to_string(bytes));
         std::sort(table_.begin(), table_.end(), [](const Entry &x, const Entry &y) { return x.name < y.name; });
         for (std::size_t i = 1; i < table_.size(); ++i)

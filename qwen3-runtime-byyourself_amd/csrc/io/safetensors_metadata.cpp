@@ -278,7 +278,7 @@ namespace qwen3
         }
         catch (const std::runtime_error &e)
         {
-            throw SafetensorsFormatError(std::string("invalid Safetensors JSON header: ") + e.what());
+            throw SafetensorsFormatError(std::string("invalid Safetensor JSON header: ") + e.what());
         }
         for (const auto &[name, verdict] : verdicts)
             if (!verdict.info)

@@ -12,9 +12,10 @@ namespace q3k
     // ---- RoPE and Q/K norm + RoPE over [tokens, heads, 128] rows ------------
 
     constexpr int kRopeHeadDim = 128;
-    // Below this many (token, head) rows a launch is small (decode): one head
-    // per lane group, so more and shorter waves fill more CUs.
-    constexpr int64_t kRopeSmallLaunchRows = 16384;
+    // Below this many (token, head) rows (kSmallLaunchBytes of 256-byte rows)
+    // a launch is small (decode): one head per lane group, so more and
+    // shorter waves fill more CUs, and write-through stores.
+    constexpr int64_t kRopeSmallLaunchRows = kSmallLaunchBytes / (2 * kRopeHeadDim);
 
     struct RopePlan
     {
@@ -22,6 +23,7 @@ namespace q3k
         int hg_q = 1;      // heads per lane of Q's waves (1, 2 or 4)
         int hg_k = 1;      // heads per lane of K's waves
         int any_heads = 0; // bit 0 (Q) / bit 1 (K): head count not a multiple of 4, rows per lane group
+        bool small = false; // a small launch: write-through stores
     };
 
     // Waves over a tensor's rows, hg heads per lane; the last one partial when
@@ -46,17 +48,23 @@ namespace q3k
     }
 
     // hk = 0 for one tensor (q3k_rope_bf16).  aligned: every tensor, the table
-    // and the norm weights 16-byte aligned.
+    // and the norm weights 16-byte aligned.  A head count that is not a
+    // multiple of 4 takes one row per lane group, with per-row tokens and
+    // positions.  (Two or four such rows per lane group, every load first,
+    // did not pay at config 4's tensor-parallel-8 shards: Q/K norm + RoPE at
+    // 4/1 heads 7.0 and 8.1 us against 7.2 us with one row, at 8/1 heads
+    // 11.3 and 12.1 us against 10.0 us.)
     inline RopePlan plan_rope(int64_t tokens, int32_t hq, int32_t hk, int32_t head_dim, bool aligned)
     {
         RopePlan p;
         if (head_dim != kRopeHeadDim || !aligned || hq <= 0 || hk < 0 || !rope_grid_ok(tokens, hq, hk))
             return p;
         p.fast = true;
+        const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kRopeSmallLaunchRows;
+        p.small = small;
         p.any_heads = (hq % kRopeHeadsPerWave != 0 ? 1 : 0) | (hk > 0 && hk % kRopeHeadsPerWave != 0 ? 2 : 0);
         if (p.any_heads != 0)
             return p;
-        const bool small = tokens * (static_cast<int64_t>(hq) + hk) < kRopeSmallLaunchRows;
         p.hg_q = small ? 1 : rope_heads_per_lane(hq);
         p.hg_k = small ? 1 : (hk == 0 ? p.hg_q : rope_heads_per_lane(hk));
         return p;

@@ -44,59 +44,73 @@ namespace q3k
             return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(a), static_cast<int>(e));
         }
 
-        // silu(g) = g / (1 + exp(-g)) for eight packed values, as
+        // The reciprocal serves a denominator below 2^126 (and NaN).
+        __device__ __forceinline__ bool rcp_ok(float den) { return den < 0x1p126f || den != den; }
+
+        // silu(g) = g / (1 + exp(-g)) for W packed words (2 W values), as
         // g * rcp(1 + exp(-g)): v_rcp_f32 is within 1 ulp, the whole
         // expression within about 3.5 ulp of the exact value.  v_rcp_f32
-        // flushes denormal results, so a group holding a denominator >= 2^126
-        // (g in [-88.72, -87.3]) or +inf (exp(-g) overflow, g < -88.72) takes
-        // the IEEE divide instead; there g / inf is the signed zero that the
-        // reference's g / (1 + expf(-g)) gives.  The branch is wave-uniform
-        // in practice and never taken on ordinary activations.
-        __device__ __forceinline__ void silu8(const uint32_t g[4], float s[8])
+        // flushes denormal results, so a denominator >= 2^126 (g in
+        // [-88.72, -87.3]) or +inf (exp(-g) overflow, g < -88.72) takes the
+        // IEEE divide instead; there g / inf is the signed zero that the
+        // reference's g / (1 + expf(-g)) gives.  The choice is per element,
+        // so the result does not depend on how elements are grouped into
+        // lanes.
+        template <int W>
+        __device__ __forceinline__ void silu_words(const uint32_t (&g)[W], float (&s)[2 * W])
         {
-            float gv[8], den[8];
+            float gv[2 * W], den[2 * W];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
+            for (int k = 0; k < W; ++k)
             {
                 gv[2 * k] = bf_lo(g[k]);
                 gv[2 * k + 1] = bf_hi(g[k]);
             }
+            bool fast = true;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 2 * W; ++j)
+            {
                 den[j] = 1.0f + exp_f32(-gv[j]);
-            const float m = fmaxf(fmaxf(fmaxf(den[0], den[1]), fmaxf(den[2], den[3])),
-                                  fmaxf(fmaxf(den[4], den[5]), fmaxf(den[6], den[7])));
-            const bool fast = m < 0x1p126f || m != m;
-            // The test is per lane, but its outcome is tested for the whole
-            // wave first: a lane-divergent if/else is issued on both sides
-            // under exec masks, and the IEEE divide would then cost every
-            // element ~12 more VALU ops.
+                fast = fast && rcp_ok(den[j]);
+            }
+            // Tested for the whole wave first: a lane-divergent if/else is
+            // issued on both sides under exec masks, and the IEEE divide would
+            // then cost every element ~12 more VALU ops.  The slow side is
+            // never taken on ordinary activations.
             if (__all(fast))
             {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
+                for (int j = 0; j < 2 * W; ++j)
                     s[j] = gv[j] * __builtin_amdgcn_rcpf(den[j]);
             }
             else
             {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    s[j] = fast ? gv[j] * __builtin_amdgcn_rcpf(den[j]) : gv[j] / den[j];
+                for (int j = 0; j < 2 * W; ++j)
+                    s[j] = rcp_ok(den[j]) ? gv[j] * __builtin_amdgcn_rcpf(den[j]) : gv[j] / den[j];
+            }
+        }
+
+        // RNE(RNE(silu(g)) * u) for W packed words.
+        template <int W>
+        __device__ __forceinline__ void silu_mul_words(const uint32_t (&g)[W], const uint32_t (&u)[W], uint32_t (&r)[W])
+        {
+            float s[2 * W];
+            silu_words<W>(g, s);
+#pragma unroll
+            for (int k = 0; k < W; ++k)
+            {
+                const uint32_t n = pack_rne(s[2 * k], s[2 * k + 1]);
+                r[k] = pack_rne(bf_lo(n) * bf_lo(u[k]), bf_hi(n) * bf_hi(u[k]));
             }
         }
 
         __device__ __forceinline__ Vec8 silu_mul8(const Vec8 &g, const Vec8 &u)
         {
-            float s[8];
-            silu8(g.d, s);
-            Vec8 r;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                const uint32_t n = pack_rne(s[2 * k], s[2 * k + 1]);
-                r.d[k] = pack_rne(bf_lo(n) * bf_lo(u.d[k]), bf_hi(n) * bf_hi(u.d[k]));
-            }
-            return r;
+            const uint32_t gw[4] = {g.d[0], g.d[1], g.d[2], g.d[3]}, uw[4] = {u.d[0], u.d[1], u.d[2], u.d[3]};
+            uint32_t rw[4];
+            silu_mul_words<4>(gw, uw, rw);
+            return Vec8{{rw[0], rw[1], rw[2], rw[3]}};
         }
 
         __device__ __forceinline__ uint16_t silu_mul1(uint16_t g, uint16_t u)
@@ -177,6 +191,53 @@ namespace q3k
             }
         }
 
+        // Small launches (a decode step): 4 elements (64 bits) per lane, so
+        // twice the waves of the 128-bit kernel with half the arithmetic each
+        // (SwiGLU at [64, 12288] replayed from a HIP graph: 2.06 against
+        // 2.20 us), and write-through stores.  The n % 4 tail is finished by
+        // a scalar pass in the first block.
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+        template <int POLICY>
+        __device__ __forceinline__ void store_words2(uint32_t *p, u32x2 v)
+        {
+            if constexpr (POLICY == kStoreStream)
+                __asm__ volatile("global_store_dwordx2 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+            else if constexpr (POLICY == kStoreThrough)
+                __asm__ volatile("global_store_dwordx2 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+            else
+                *reinterpret_cast<u32x2 *>(p) = v;
+        }
+
+        template <int OP, int NTM>
+        __global__ __launch_bounds__(kBlock) void binary_half_kernel(const uint16_t *a, const uint16_t *b,
+                                                                      uint16_t *out, int64_t nhalf, int64_t n)
+        {
+            const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+            if (j < nhalf)
+            {
+                const u32x2 *ap = reinterpret_cast<const u32x2 *>(a) + j;
+                const u32x2 *bp = reinterpret_cast<const u32x2 *>(b) + j;
+                const u32x2 x = nt_load(NTM) ? __builtin_nontemporal_load(ap) : *ap;
+                const u32x2 y = nt_load(NTM) ? __builtin_nontemporal_load(bp) : *bp;
+                const uint32_t xw[2] = {x.x, x.y}, yw[2] = {y.x, y.y};
+                uint32_t rw[2];
+                if constexpr (OP == 0)
+                    silu_mul_words<2>(xw, yw, rw);
+                else
+                {
+                    rw[0] = add2(xw[0], yw[0]);
+                    rw[1] = add2(xw[1], yw[1]);
+                }
+                store_words2<nt_store(NTM)>(reinterpret_cast<uint32_t *>(out) + 2 * j, u32x2{rw[0], rw[1]});
+            }
+            if (blockIdx.x == 0)
+            {
+                for (int64_t e = nhalf * 4 + threadIdx.x; e < n; e += kBlock)
+                    out[e] = apply1<OP>(a[e], b[e]);
+            }
+        }
+
         template <int OP>
         __global__ __launch_bounds__(kBlock) void binary_scalar_kernel(
             const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n)
@@ -195,7 +256,20 @@ namespace q3k
             constexpr int PR = OP == 0 ? kPrioSilu : 0;
             constexpr bool REMAP = OP == 0 ? kRemapSilu : kRemapAdd;
             const int64_t nvec = n / 8;
-            if (aligned16(a) && aligned16(b) && aligned16(out) && binary_vec_fits(n, U))
+            const bool small = n * 2 <= kSmallLaunchBytes;
+            if (OP == 0 && small && aligned_to(a, 8) && aligned_to(b, 8) && aligned_to(out, 8))
+            {
+                // at most 2M elements: the grid fits one dispatch
+                const int64_t nhalf = n / 4;
+                const dim3 grid(static_cast<unsigned>(nhalf > 0 ? blocks_for(nhalf, kBlock) : 1));
+                binary_half_kernel<OP, ntm_small(NTM)><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nhalf, n);
+            }
+            else if (small && aligned16(a) && aligned16(b) && aligned16(out))
+            {
+                const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U)));
+                binary_vec_kernel<OP, U, ntm_small(NTM), PR, REMAP><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);
+            }
+            else if (aligned16(a) && aligned16(b) && aligned16(out) && binary_vec_fits(n, U))
             {
                 const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U)));
                 binary_vec_kernel<OP, U, NTM, PR, REMAP><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);

@@ -17,6 +17,10 @@ namespace q3k
     // Blocks of 256 threads (four waves) unless stated otherwise.
     constexpr int kBlock = 256;
 
+    // A launch that writes at most this many bytes is small (a decode step):
+    // its kernels take their small-launch shapes and store policy.
+    constexpr int64_t kSmallLaunchBytes = int64_t{4} << 20;
+
     // Whether `blocks` blocks of `threads` threads fit one dispatch.
     inline bool launch_fits(int64_t blocks, int64_t threads)
     {

@@ -46,19 +46,32 @@ namespace q3k
         return r;
     }
 
-    // NT = true: a streaming store with device scope (`nt sc1`).  The eight
-    // XCDs of MI355X each have their own L2, and a store at device scope is
-    // written through it instead of leaving a dirty line that the end of the
-    // kernel has to write back before the next kernel may start.  Measured on
-    // a 64 MB -> 64 MB copy: 72.8% of peak HBM with `nt` alone, 76.1% with
-    // `nt sc1`.  No compiler builtin sets sc1 on a global store, hence the
-    // asm.  A 128-bit store reads its data VGPRs a few cycles after it
-    // issues, and a VALU write to them in that window corrupts the store; for
-    // its own stores the compiler keeps such a write two wait states back
-    // (`s_nop 1`), but it cannot see into the asm, so the asm carries those
-    // wait states itself.  A store returns nothing, so there is no counter
-    // wait for the compiler to track.
-    template <bool NT>
+    // Store policies of the 128-bit store.
+    //   kStoreStream (`nt sc1`): a streaming store with device scope.  The
+    //     eight XCDs of MI355X each have their own L2, and a store at device
+    //     scope is written through it instead of leaving a dirty line that the
+    //     end of the kernel has to write back before the next kernel may
+    //     start.  Measured on a 64 MB -> 64 MB copy: 72.8% of peak HBM with
+    //     `nt` alone, 76.1% with `nt sc1`.
+    //   kStoreThrough (`sc1`): written through at device scope without the
+    //     non-temporal hint.  For launches of a few MB that write over what
+    //     they have just read (the in-place ops at decode sizes) it is
+    //     faster: a 1 MB in-place copy replayed from a HIP graph took 1.97 us
+    //     against 2.18 us with `nt sc1`, add + RMSNorm [64, 4096] 2.41 against
+    //     2.69 us; out of place the two are equal, and at 64 MB `nt sc1` is 2%
+    //     faster.
+    // No compiler builtin sets sc1 on a global store, hence the asm.  A
+    // 128-bit store reads its data VGPRs a few cycles after it issues, and a
+    // VALU write to them in that window corrupts the store; for its own
+    // stores the compiler keeps such a write two wait states back (`s_nop 1`),
+    // but it cannot see into the asm, so the asm carries those wait states
+    // itself.  A store returns nothing, so there is no counter wait for the
+    // compiler to track.
+    constexpr int kStorePlain = 0;
+    constexpr int kStoreStream = 1;
+    constexpr int kStoreThrough = 2;
+
+    template <int POLICY>
     __device__ __forceinline__ void store8(Vec8 *p, const Vec8 &r)
     {
         u32x4 v;
@@ -66,8 +79,10 @@ namespace q3k
         v.y = r.d[1];
         v.z = r.d[2];
         v.w = r.d[3];
-        if constexpr (NT)
+        if constexpr (POLICY == kStoreStream)
             __asm__ volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+        else if constexpr (POLICY == kStoreThrough)
+            __asm__ volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
         else
             *reinterpret_cast<u32x4 *>(p) = v;
     }
@@ -140,18 +155,21 @@ namespace q3k
         return v;
     }
 
-    // Sum of the squares of eight bf16 values, pairwise (exact products).
+    // Sum of the squares of eight bf16 values in element order, one product
+    // and seven fused multiply-adds (each square is exact in fp32).  The
+    // fused Q/K norm + RoPE kernel runs four heads per lane through this;
+    // the pairwise form cost it 6% (28.8 against 27.0 us at config 4).
     __device__ __forceinline__ float sum_sq8(const Vec8 &x)
     {
-        float s[4];
+        float s = bf_lo(x.d[0]) * bf_lo(x.d[0]);
+        s = __builtin_fmaf(bf_hi(x.d[0]), bf_hi(x.d[0]), s);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 1; i < 4; ++i)
         {
-            const float a = bf_lo(x.d[i]);
-            const float b = bf_hi(x.d[i]);
-            s[i] = a * a + b * b;
+            s = __builtin_fmaf(bf_lo(x.d[i]), bf_lo(x.d[i]), s);
+            s = __builtin_fmaf(bf_hi(x.d[i]), bf_hi(x.d[i]), s);
         }
-        return (s[0] + s[1]) + (s[2] + s[3]);
+        return s;
     }
 
     // 1 / sqrt(sum * inv_n + eps) with the hardware reciprocal square root
@@ -178,9 +196,18 @@ namespace q3k
         return (block % 8) * per + block / 8;
     }
 
-    // NT mode bits of a kernel: bit 0 = non-temporal loads, bit 1 = non-temporal stores.
+    // NT mode bits of a kernel: bit 0 = non-temporal loads, bit 1 = streaming
+    // stores (`nt sc1`), bit 2 = write-through stores (`sc1`, small launches;
+    // takes precedence over bit 1).
+    constexpr int kNtmThroughStores = 4;
     constexpr bool nt_load(int ntm) { return (ntm & 1) != 0; }
-    constexpr bool nt_store(int ntm) { return (ntm & 2) != 0; }
+    constexpr int nt_store(int ntm)
+    {
+        return (ntm & kNtmThroughStores) != 0 ? kStoreThrough : (ntm & 2) != 0 ? kStoreStream : kStorePlain;
+    }
+    // The mode bits of a small launch (at most kSmallLaunchBytes written):
+    // the loads of `ntm`, write-through stores.
+    constexpr int ntm_small(int ntm) { return (ntm & 1) | kNtmThroughStores; }
 
     // y = RNE(RNE(x * inv) * w) for eight elements.
     __device__ __forceinline__ Vec8 norm_scale8(const Vec8 &x, const Vec8 &w, float inv)

@@ -375,6 +375,21 @@ namespace q3k
             hipStream_t stream;
         };
 
+        // A launch that writes at most kSmallLaunchBytes of y (a decode step)
+        // stores with write-through (`sc1`) instead of streaming stores.
+        inline bool small_launch(const Launch &l) { return l.rows * l.nvec * 16 <= kSmallLaunchBytes; }
+
+        template <int G, int VPT, int RPG, int MODE, int NTM>
+        void launch_rows_ntm(const Launch &l, const dim3 &grid)
+        {
+            if (l.nvec == G * VPT)
+                rms_rows_kernel<G, VPT, RPG, MODE, NTM, true><<<grid, dim3(kBlock), 0, l.stream>>>(
+                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            else
+                rms_rows_kernel<G, VPT, RPG, MODE, NTM, false><<<grid, dim3(kBlock), 0, l.stream>>>(
+                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+        }
+
         template <int G, int VPT, int RPG, int MODE>
         bool launch_rows_rpg(const Launch &l)
         {
@@ -382,12 +397,10 @@ namespace q3k
             if (!rms_rows_fit(l.rows, G))
                 return false;
             const dim3 grid(static_cast<unsigned>(blocks_for(l.rows, kRowsPerBlock)));
-            if (l.nvec == G * VPT)
-                rms_rows_kernel<G, VPT, RPG, MODE, ntm_rows<MODE>(), true><<<grid, dim3(kBlock), 0, l.stream>>>(
-                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            if (small_launch(l))
+                launch_rows_ntm<G, VPT, RPG, MODE, ntm_small(ntm_rows<MODE>())>(l, grid);
             else
-                rms_rows_kernel<G, VPT, RPG, MODE, ntm_rows<MODE>(), false><<<grid, dim3(kBlock), 0, l.stream>>>(
-                    l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+                launch_rows_ntm<G, VPT, RPG, MODE, ntm_rows<MODE>()>(l, grid);
             return true;
         }
 
@@ -414,18 +427,27 @@ namespace q3k
             return launch_rows_rpg<G, VPT, 1, MODE>(l);
         }
 
+        template <int WPR, int VPT, int MODE, int NTM>
+        void launch_block_ntm(const Launch &l)
+        {
+            const dim3 grid(static_cast<unsigned>(l.rows)), block(WPR * kWave);
+            if (l.nvec == WPR * kWave * VPT)
+                rms_block_kernel<WPR, VPT, MODE, NTM, prio_block<MODE>(), kRemapRows, true>
+                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            else
+                rms_block_kernel<WPR, VPT, MODE, NTM, prio_block<MODE>(), kRemapRows, false>
+                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+        }
+
         template <int WPR, int VPT, int MODE>
         bool launch_block(const Launch &l)
         {
             if (!rms_block_fits(l.rows, WPR))
                 return false;
-            const dim3 grid(static_cast<unsigned>(l.rows)), block(WPR * kWave);
-            if (l.nvec == WPR * kWave * VPT)
-                rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, true>
-                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+            if (small_launch(l))
+                launch_block_ntm<WPR, VPT, MODE, ntm_small(ntm_block<MODE>())>(l);
             else
-                rms_block_kernel<WPR, VPT, MODE, ntm_block<MODE>(), prio_block<MODE>(), kRemapRows, false>
-                    <<<grid, block, 0, l.stream>>>(l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
+                launch_block_ntm<WPR, VPT, MODE, ntm_block<MODE>()>(l);
             return true;
         }
 

@@ -100,6 +100,82 @@ namespace q3k
         constexpr int kVecPerHead = kHeadDim / 8;
         constexpr int kHeadStride = kHeadsPerWave * kVecPerHead;  // Vec8s between a lane's heads
 
+        // cos and sin of pairs 8(l%8) .. +7 of position `pos` for the lane
+        // (l = lane16); first-half lanes use -sin so that both halves compute
+        // own * cos + partner * sin'.
+        __device__ __forceinline__ void table_row(const float *table, int64_t pos, int lane16, float (&cs)[8],
+                                                  float (&sn)[8])
+        {
+            const F4 *crow = reinterpret_cast<const F4 *>(table + (pos * kHalf + (lane16 % 8) * 8) * 2);
+            const uint32_t sign = lane16 < 8 ? 0x80000000u : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const F4 t = crow[i];
+                cs[2 * i] = t.v[0];
+                sn[2 * i] = __uint_as_float(__float_as_uint(t.v[1]) ^ sign);
+                cs[2 * i + 1] = t.v[2];
+                sn[2 * i + 1] = __uint_as_float(__float_as_uint(t.v[3]) ^ sign);
+            }
+        }
+
+        // The lane's 8 norm weights (bf16 -> fp32).
+        __device__ __forceinline__ void norm_weights(const uint16_t *w, int lane16, float (&wf)[8])
+        {
+            const Vec8 wv = reinterpret_cast<const Vec8 *>(w)[lane16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                wf[2 * j] = bf_lo(wv.d[j]);
+                wf[2 * j + 1] = bf_hi(wv.d[j]);
+            }
+        }
+
+        // One head's 8 elements of this lane: with NORM, rms_norm over the
+        // head (128 values in 16 lanes, two roundings), then the rotation of
+        // the rounded values; the partner element (lane ^ 8) comes through
+        // DPP, folded into the multiply.  Every lane of the 16-lane group must
+        // run it together.
+        template <bool NORM>
+        __device__ __forceinline__ Vec8 rotate_head(const Vec8 &x, const float (&wf)[8], const float (&cs)[8],
+                                                    const float (&sn)[8], float eps)
+        {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                v[2 * j] = bf_lo(x.d[j]);
+                v[2 * j + 1] = bf_hi(x.d[j]);
+            }
+            if constexpr (NORM)
+            {
+                // the sum of squares in the order of the plain RMSNorm kernel's
+                // 128-wide rows (sum_sq8, then the 16 lanes), so that the fused
+                // op equals rms_norm + RoPE bit for bit
+                const float total = group_sum<16>(sum_sq8(x));
+                const float inv = inverse_rms(total, 1.0f / static_cast<float>(kHeadDim), eps);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                {
+                    const uint32_t n = pack_rne(v[2 * j] * inv, v[2 * j + 1] * inv);
+                    const uint32_t y = pack_rne(bf_lo(n) * wf[2 * j], bf_hi(n) * wf[2 * j + 1]);
+                    v[2 * j] = bf_lo(y);
+                    v[2 * j + 1] = bf_hi(y);
+                }
+            }
+            Vec8 r;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const float a0 = v[2 * j] * cs[2 * j];
+                const float b0 = dpp_f<kDppRowRor8>(v[2 * j]) * sn[2 * j];
+                const float a1 = v[2 * j + 1] * cs[2 * j + 1];
+                const float b1 = dpp_f<kDppRowRor8>(v[2 * j + 1]) * sn[2 * j + 1];
+                r.d[j] = pack_rne(a0 + b0, a1 + b1);
+            }
+            return r;
+        }
+
         // One wave = 4 * HG consecutive heads of one token (heads % (4 * HG)
         // == 0): lane l of the wave works on heads l/16 + 4i, i < HG, of
         // `src`/`dst` (already offset to the wave's first head and the lane's
@@ -145,71 +221,12 @@ namespace q3k
 
             float wf[8];
             if constexpr (NORM)
-            {
-                const Vec8 wv = reinterpret_cast<const Vec8 *>(w)[lane16];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                {
-                    wf[2 * j] = bf_lo(wv.d[j]);
-                    wf[2 * j + 1] = bf_hi(wv.d[j]);
-                }
-            }
-            // cos and sin of pairs 8(l%8) .. +7; first-half lanes use -sin so
-            // that both halves compute own * cos + partner * sin'.
-            const F4 *crow = reinterpret_cast<const F4 *>(table + (pos * kHalf + (lane16 % 8) * 8) * 2);
-            const uint32_t sign = lane16 < 8 ? 0x80000000u : 0u;
+                norm_weights(w, lane16, wf);
             float cs[8], sn[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                const F4 t = crow[i];
-                cs[2 * i] = t.v[0];
-                sn[2 * i] = __uint_as_float(__float_as_uint(t.v[1]) ^ sign);
-                cs[2 * i + 1] = t.v[2];
-                sn[2 * i + 1] = __uint_as_float(__float_as_uint(t.v[3]) ^ sign);
-            }
-
+            table_row(table, pos, lane16, cs, sn);
 #pragma unroll
             for (int i = 0; i < HG; ++i)
-            {
-                float v[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                {
-                    v[2 * j] = bf_lo(x[i].d[j]);
-                    v[2 * j + 1] = bf_hi(x[i].d[j]);
-                }
-                if constexpr (NORM)
-                {
-                    // rms_norm over the head (128 values in 16 lanes), two roundings
-                    float partial = v[0] * v[0];
-#pragma unroll
-                    for (int j = 1; j < 8; ++j)
-                        partial = __builtin_fmaf(v[j], v[j], partial);
-                    const float total = group_sum<16>(partial);
-                    const float inv = inverse_rms(total, 1.0f / static_cast<float>(kHeadDim), eps);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                    {
-                        const uint32_t n = pack_rne(v[2 * j] * inv, v[2 * j + 1] * inv);
-                        const uint32_t y = pack_rne(bf_lo(n) * wf[2 * j], bf_hi(n) * wf[2 * j + 1]);
-                        v[2 * j] = bf_lo(y);
-                        v[2 * j + 1] = bf_hi(y);
-                    }
-                }
-                // partner value (lane ^ 8) through DPP, folded into the multiply
-                Vec8 r;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                {
-                    const float a0 = v[2 * j] * cs[2 * j];
-                    const float b0 = dpp_f<kDppRowRor8>(v[2 * j]) * sn[2 * j];
-                    const float a1 = v[2 * j + 1] * cs[2 * j + 1];
-                    const float b1 = dpp_f<kDppRowRor8>(v[2 * j + 1]) * sn[2 * j + 1];
-                    r.d[j] = pack_rne(a0 + b0, a1 + b1);
-                }
-                store8<nt_store(NTM)>(dst + i * kHeadStride, r);
-            }
+                store8<nt_store(NTM)>(dst + i * kHeadStride, rotate_head<NORM>(x[i], wf, cs, sn, eps));
             if constexpr (COPY_V)
             {
 #pragma unroll
@@ -394,15 +411,20 @@ namespace q3k
         }
 
         template <bool NORM, bool KV, int HGQ, int HGK, int ANYH = 0>
-        void launch_heads_hg(uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq, int32_t hk,
-                             int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv, hipStream_t stream)
+        void launch_heads_hg(bool small, uint16_t *q, uint16_t *k, const uint16_t *qw, const uint16_t *kw, int32_t hq,
+                             int32_t hk, int64_t tokens, const RopeShape &rs, float eps, const KvDest &kv,
+                             hipStream_t stream)
         {
             constexpr int NTM = NORM ? kNtmNormRope : kNtmRope;
             const int64_t q_waves = rope_waves(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : rope_waves(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
-                <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            if (small)
+                rope_heads_kernel<NORM, ntm_small(NTM), HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
+                    <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            else
+                rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
+                    <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
         // The instance the plan (plan_rope) names: heads per lane of Q and K, or
@@ -415,24 +437,24 @@ namespace q3k
             if (plan.any_heads != 0)
             {
                 if (plan.any_heads == 1)
-                    launch_heads_hg<NORM, KV, 1, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                    launch_heads_hg<NORM, KV, 1, 1, 1>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 else if (plan.any_heads == 2)
-                    launch_heads_hg<NORM, KV, 1, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                    launch_heads_hg<NORM, KV, 1, 1, 2>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 else
-                    launch_heads_hg<NORM, KV, 1, 1, 3>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
+                    launch_heads_hg<NORM, KV, 1, 1, 3>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream);
                 return;
             }
             switch (plan.hg_q * 10 + plan.hg_k)
             {
-            case 44: launch_heads_hg<NORM, KV, 4, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 42: launch_heads_hg<NORM, KV, 4, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 41: launch_heads_hg<NORM, KV, 4, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 24: launch_heads_hg<NORM, KV, 2, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 22: launch_heads_hg<NORM, KV, 2, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 21: launch_heads_hg<NORM, KV, 2, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 14: launch_heads_hg<NORM, KV, 1, 4>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            case 12: launch_heads_hg<NORM, KV, 1, 2>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
-            default: launch_heads_hg<NORM, KV, 1, 1>(q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 44: launch_heads_hg<NORM, KV, 4, 4>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 42: launch_heads_hg<NORM, KV, 4, 2>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 41: launch_heads_hg<NORM, KV, 4, 1>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 24: launch_heads_hg<NORM, KV, 2, 4>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 22: launch_heads_hg<NORM, KV, 2, 2>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 21: launch_heads_hg<NORM, KV, 2, 1>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 14: launch_heads_hg<NORM, KV, 1, 4>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            case 12: launch_heads_hg<NORM, KV, 1, 2>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
+            default: launch_heads_hg<NORM, KV, 1, 1>(plan.small, q, k, qw, kw, hq, hk, tokens, rs, eps, kv, stream); break;
             }
         }
     } // namespace

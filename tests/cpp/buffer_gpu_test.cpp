@@ -3,6 +3,8 @@
 // moves, a failing allocation, and the current device left unchanged.
 #include "gpu_util.hpp"
 
+#include <cstdlib>
+#include <string>
 #include <utility>
 
 using test::require;
@@ -54,6 +56,24 @@ static void body()
     g2.copy_from(g);
     require(test::to_host<std::int32_t>(g2)[7] == 80, "GPU copy_from");
     require(test::current_device() == before, "tensor ops changed the current device");
+
+    // the small-block cache: a block of a size class just freed is reused without hipMalloc; with
+    // QWEN3_DEVICE_BLOCK_CACHE=0 every small Buffer calls hipMalloc (and its destruction hipFree)
+    const char *env = std::getenv("QWEN3_DEVICE_BLOCK_CACHE");
+    const bool cache_on = env == nullptr || std::string(env) != "0";
+    {
+        qwen3::Buffer warm{3000, qwen3::Device::cuda(0)};
+    }
+    const std::uint64_t n0 = qwen3::device_allocation_count();
+    for (int i = 0; i < 4; ++i)
+    {
+        qwen3::Buffer small{2500 + static_cast<std::size_t>(i), qwen3::Device::cuda(0)};
+        require(small.data() != nullptr, "small device buffer");
+    }
+    const std::uint64_t made = qwen3::device_allocation_count() - n0;
+    require(cache_on ? made == 0 : made == 4,
+            std::string("small-block cache ") + (cache_on ? "on" : "off") + ": " + std::to_string(made) +
+                " hipMalloc calls for 4 buffers");
 }
 
 int main() { return test::run("GPU Buffer/Tensor test", body); }

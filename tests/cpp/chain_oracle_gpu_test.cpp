@@ -16,7 +16,8 @@
 //   a slice of config 4 (Qwen3-8B shapes, 2 sequences x 128 tokens at
 //   positions 64..191 of the 2048-position table).
 // Residual streams must be bit-exact; every other output inside the oracle's
-// band widened by one bf16 ulp.  Each comparison prints a PARITY line (JSON:
+// band widened by one bf16 ulp; and the two chains' outputs equal bit for
+// bit.  Each comparison prints a PARITY line (JSON:
 // case, elements, failures, ulp histogram) that the pytest runner adds to the
 // parity report.
 #include "gpu_util.hpp"
@@ -136,6 +137,7 @@ namespace
         Tensor gqn = gpu(qn, Shape{kD}), gkn = gpu(kn, Shape{kD}), gpost = gpu(post, Shape{w.H}), gnext = gpu(next, Shape{w.H});
         const qwen3::NonGemmLayerWeights weights{gqn, gkn, gpost, gnext};
         Tensor gattn = gpu(attn, hs), ggate = gpu(gate, is), gup = gpu(up, is), gmlp = gpu(mlp, hs);
+        std::vector<std::vector<uint16_t>> first;
         for (const bool fused : {true, false})
         {
             const std::string tag = std::string(w.name) + (fused ? " fused" : " unfused");
@@ -144,12 +146,20 @@ namespace
             const auto out = fused ? qwen3::qwen3_non_gemm_layer(tensors, weights, cache, w.Hq, w.Hkv, w.start, kEps)
                                    : qwen3::qwen3_non_gemm_layer_unfused(tensors, weights, cache, w.Hq, w.Hkv,
                                                                          w.start, kEps);
-            report(tag + " residual", test::to_host<uint16_t>(h), oh, nullptr, nullptr);
-            report(tag + " query", test::to_host<uint16_t>(q), oq, &qlo, &qhi);
-            report(tag + " key", test::to_host<uint16_t>(k), ok, &klo, &khi);
-            report(tag + " mlp_input", test::to_host<uint16_t>(out.mlp_input), y1, &y1lo, &y1hi);
-            report(tag + " activation", test::to_host<uint16_t>(out.activation), act, &alo, &ahi);
-            report(tag + " next_input", test::to_host<uint16_t>(out.next_input), y2, &y2lo, &y2hi);
+            const std::vector<std::vector<uint16_t>> got{
+                test::to_host<uint16_t>(h), test::to_host<uint16_t>(q), test::to_host<uint16_t>(k),
+                test::to_host<uint16_t>(out.mlp_input), test::to_host<uint16_t>(out.activation),
+                test::to_host<uint16_t>(out.next_input)};
+            report(tag + " residual", got[0], oh, nullptr, nullptr);
+            report(tag + " query", got[1], oq, &qlo, &qhi);
+            report(tag + " key", got[2], ok, &klo, &khi);
+            report(tag + " mlp_input", got[3], y1, &y1lo, &y1hi);
+            report(tag + " activation", got[4], act, &alo, &ahi);
+            report(tag + " next_input", got[5], y2, &y2lo, &y2hi);
+            if (fused)
+                first = got;
+            else
+                require(got == first, std::string(w.name) + ": the unfused chain differs from the fused one");
         }
     }
 

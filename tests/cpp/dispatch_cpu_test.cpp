@@ -35,12 +35,12 @@ namespace
                 require(p.fast, what + ": generic kernels chosen");
                 const int any = (h.hq % 4 != 0 ? 1 : 0) | (h.hkv % 4 != 0 ? 2 : 0);
                 require(p.any_heads == any, what + ": rows per lane group only for head counts not a multiple of 4");
+                const bool small = tokens * (h.hq + h.hkv) < kRopeSmallLaunchRows;
                 if (any != 0)
                 {
                     require(p.hg_q == 1 && p.hg_k == 1, what + ": one head per lane group");
                     continue;
                 }
-                const bool small = tokens * (h.hq + h.hkv) < kRopeSmallLaunchRows;
                 const int want_q = small ? 1 : (h.hq % 16 == 0 ? 4 : h.hq % 8 == 0 ? 2 : 1);
                 const int want_k = small ? 1 : (h.hkv % 16 == 0 ? 4 : h.hkv % 8 == 0 ? 2 : 1);
                 require(p.hg_q == want_q && p.hg_k == want_k, what + ": heads per lane");

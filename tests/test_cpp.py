@@ -40,3 +40,10 @@ def test_cpp_cpu(name):
 @pytest.mark.parametrize("name", GPU_TESTS)
 def test_cpp_gpu(name):
     _run(name, timeout=300)
+
+
+@pytest.mark.gpu
+def test_cpp_gpu_block_cache_off():
+    """Buffer with the small-block cache turned off (QWEN3_DEVICE_BLOCK_CACHE=0): every small block goes through
+    hipMalloc and hipFree, as the reference's Buffer does."""
+    _run("buffer_gpu_test", env=dict(os.environ, QWEN3_DEVICE_BLOCK_CACHE="0"), timeout=300)

@@ -159,7 +159,11 @@ def test_elementwise_kat(q3k, hip, oracle):
 
 
 @pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (8, 0), (9, 0), (1000, 0), (8191, 0), (65536 + 3, 0),
-                                      (1 << 20, 0), (4097, 2), (1 << 16, 2)])
+                                      (1 << 20, 0), (4097, 2), (1 << 16, 2),
+                                      # 8-byte aligned: the small-launch kernel's 64-bit accesses
+                                      (1001, 8), ((1 << 20) + 3, 8),
+                                      # above the small-launch size (4 MiB written): the 128-bit kernels
+                                      ((3 << 20) + 5, 0), ((3 << 20) + 1, 8)])
 def test_elementwise_shapes(q3k, hip, oracle, synth, n, offset):
     name = f"elementwise n={n} offset={offset}"
     announce(name)
@@ -170,11 +174,14 @@ def test_elementwise_shapes(q3k, hip, oracle, synth, n, offset):
     check_band(oracle, "silu " + name, run_binary(q3k, hip, "silu", a, b, offset), prim, lo, hi)
 
 
-def test_silu_extremes(q3k, hip, oracle, synth):
-    announce("silu extremes")
+@pytest.mark.parametrize("repeats", [9, 140003])
+def test_silu_extremes(q3k, hip, oracle, synth, repeats):
+    """Denominators past 2^126 and infinite ones (the IEEE-divide side) mixed with ordinary values in one lane:
+    144 elements (the small-launch kernel and its scalar tail) and 2.2M (the 128-bit kernel)."""
+    announce(f"silu extremes x{repeats}")
     vals = np.array([-100.0, -89.0, -88.0, -87.0, -20.0, -1e-30, 0.0, 1e-30, 20.0, 88.0, 100.0, 3.0e38, -3.0e38,
                      1e-38, -1e-38, -0.0], np.float32)
-    g = synth.f32_to_bf16(np.tile(vals, 9))  # 144 elements: vector body and scalar tail
+    g = synth.f32_to_bf16(np.tile(vals, repeats))
     u = np.full(g.shape, 0x3F80, np.uint16)
     prim, lo, hi = oracle.silu_mul(g, u)
     check_band(oracle, "silu extremes", run_binary(q3k, hip, "silu", g, u), prim, lo, hi)
@@ -233,7 +240,9 @@ def test_rope_kat(q3k, hip, oracle):
                                                       (3, 4, 6, 128, 1, 0),
                                                       # head counts that are not a multiple of 4: waves span tokens,
                                                       # and the last wave is partial
-                                                      (3, 7, 1, 128, 2, 0), (2, 5, 3, 128, 0, 0)])
+                                                      (3, 7, 1, 128, 2, 0), (2, 5, 3, 128, 0, 0),
+                                                      # the same at a larger size, partial last wave
+                                                      (2, 9000, 3, 128, 5, 0)])
 def test_rope_shapes(q3k, hip, oracle, synth, B, S, heads, D, start, offset):
     name = f"rope B={B} S={S} heads={heads} D={D} start={start} offset={offset}"
     announce(name)
@@ -263,6 +272,9 @@ def test_rope_positions_overload(q3k, hip, oracle, synth):
     (2, 64, 64, 8, 128, 9, 0, False),    # config 5 heads
     (4, 64, 4, 1, 128, 0, 0, False),     # a tensor-parallel-8 shard: K head count not a multiple of 4
     (3, 7, 6, 2, 128, 1, 0, False),      # both head counts not multiples of 4, partial last waves
+    (4, 1024, 4, 1, 128, 0, 0, False),   # a tensor-parallel-8 shard, larger
+    (3, 1001, 6, 2, 128, 1, 0, False),   # rows per lane group with partial last waves, larger
+    (4096, 1, 5, 3, 128, 0, 0, True),    # rows per lane group with a position per sequence
     (2, 9, 4, 4, 64, 2, 0, False),       # head_dim 64: the generic kernel, two launches
     (1, 7, 8, 8, 128, 0, 2, False)])     # unaligned: the generic kernel
 def test_rope_qk_one_launch(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, offset, with_pos):
@@ -302,7 +314,9 @@ def test_rope_qk_one_launch(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, of
                                                        # not a multiple of 4, with partial last waves
                                                        (4, 2048, 4, 1, 128, 0, 0), (3, 7, 5, 3, 128, 1, 0),
                                                        (1, 9, 4, 1, 128, 0, 0), (2, 3, 1, 1, 128, 0, 0),
-                                                       (1, 11, 2, 2, 128, 4, 0), (2, 9, 6, 4, 128, 3, 0)])
+                                                       (1, 11, 2, 2, 128, 4, 0), (2, 9, 6, 4, 128, 3, 0),
+                                                       # the same at larger sizes, partial last waves
+                                                       (2, 1500, 5, 3, 128, 0, 0), (1, 7000, 2, 1, 128, 9, 0)])
 def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, offset):
     name = f"qk_norm_rope B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} start={start} offset={offset}"
     announce(name)
@@ -316,6 +330,28 @@ def test_qk_norm_rope_shapes(q3k, hip, oracle, synth, B, S, Hq, Hkv, D, start, o
     pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache, start)
     check_band(oracle, name + " q", gq, pq, lq, hq)
     check_band(oracle, name + " k", gk, pk, lk, hk)
+
+
+def test_qk_norm_rope_rows_positions(q3k, hip, oracle, synth):
+    """Head counts that are not a multiple of 4 (rows per lane group) with a position per sequence (decode at a
+    tensor-parallel shard of many sequences), some of them outside the table: those heads become NaN, every other
+    head is inside the band."""
+    B, S, Hq, Hkv, D, P = 8192, 1, 4, 1, 128, 4096
+    announce("qk_norm_rope rows per lane group, positions")
+    cache = q3k.build_rope_cache(P, D, 1.0e6)
+    q = synth.normal_bf16(116, 1, (B, S, Hq * D))
+    k = synth.normal_bf16(117, 1, (B, S, Hkv * D))
+    qw = synth.normal_bf16(118, D, (D,), mean=1.0, std=0.1)
+    kw = synth.normal_bf16(119, D, (D,), mean=1.0, std=0.1)
+    pos = synth.uniform_positions(116, 2, B * S, P)
+    pos[[5, 77, 4000]] = [P, -1, P + 100]
+    gq, gk = run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache, positions=pos)
+    pq, lq, hq = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, cache, positions=pos)
+    pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache, positions=pos)
+    check_band(oracle, "rows positions q", gq, pq, lq, hq)
+    check_band(oracle, "rows positions k", gk, pk, lk, hk)
+    for t in (5, 77, 4000):
+        assert np.all((gq[t] & 0x7FFF) > 0x7F80) and np.all((gk[t] & 0x7FFF) > 0x7F80), t
 
 
 def _special_rows(synth, rows, n, seed):

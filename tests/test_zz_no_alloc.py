@@ -66,3 +66,36 @@ def test_noalloc_argmax_argument_errors(q3k, hip):
     q3k.argmax_noalloc(None, None, 0, 8, 8)   # no rows: nothing to do
     X.free()
     O.free()
+
+
+def test_noalloc_argmax_captured_in_graph(q3k, hip, oracle, synth):
+    """The entry point captured into a HIP graph, for callers that record their decode step: the first call on
+    the GPU (made eagerly, before the capture) resolves the array's device address; the captured call then
+    replays three times, each replay preceded by an eager call on other logits that overwrites the same array,
+    and every replay's result equals the oracle's."""
+    rows, N = 9, 40000
+    rows2, N2 = 2, 151936
+    assert q3k.argmax_workspace_bytes(rows, N) > 0 and q3k.argmax_workspace_bytes(rows2, N2) > 0, "sliced shapes"
+    announce(f"argmax noalloc in a graph: rows={rows} N={N}, eager rows={rows2} N={N2} between replays")
+    x, x2 = _logits(synth, 10, rows, N), _logits(synth, 11, rows2, N2)
+    want, want2 = oracle.argmax(x).view(np.uint32), oracle.argmax(x2).view(np.uint32)
+    X, X2 = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(x2)
+    O, O2 = hip.DeviceBuffer(rows * 4), hip.DeviceBuffer(rows2 * 4)
+    stream = hip.Stream()
+    q3k.argmax_noalloc(X, O, rows, N, N, stream)   # the first call on this GPU: before any capture
+    stream.synchronize()
+    graph = hip.Graph(stream, lambda: q3k.argmax_noalloc(X, O, rows, N, N, stream))
+    try:
+        for replay in range(3):
+            O.fill_bytes(0xFF)
+            q3k.argmax_noalloc(X2, O2, rows2, N2, N2, stream)
+            stream.synchronize()
+            check_exact(f"eager call before replay {replay}", O2.download(np.int32, (rows2,)).view(np.uint32), want2)
+            graph.launch(stream)
+            stream.synchronize()
+            check_exact(f"graph replay {replay}", O.download(np.int32, (rows,)).view(np.uint32), want)
+    finally:
+        graph.destroy()
+        for b in (X, X2, O, O2):
+            b.free()
+        stream.destroy()
