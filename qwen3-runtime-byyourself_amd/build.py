@@ -58,12 +58,15 @@ CXX_FLAGS = [
 ]
 RPATH = [f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}", "-Wl,-rpath,$ORIGIN"]
 
-# Per-file device flags.  Element-wise kernels: arguments preloaded into SGPRs
-# at wave launch instead of loaded from the kernarg segment (SwiGLU
-# [64, 12288] replayed from a HIP graph: 2.43 against 2.55 us; [8192, 1536]:
-# 13.8 against 14.1 us).  Not for the RMSNorm and RoPE files: config 4's Q/K
-# norm + RoPE ran 28.8 against 28.1 us with it.
-FILE_FLAGS = {"elementwise.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+# Per-file device flags.  Element-wise and RoPE kernels: arguments preloaded
+# into SGPRs at wave launch instead of loaded from the kernarg segment
+# (SwiGLU [64, 12288] replayed from a HIP graph: 2.43 against 2.55 us;
+# [8192, 1536]: 13.8 against 14.1 us; config 4's Q/K norm + RoPE 27.1 against
+# 27.4 us, RoPE over Q and K 26.8 against 27.1 us, in alternating runs on one
+# box).  Not for the RMSNorm file: add + RMSNorm at config 4 ran 43.1 against
+# 42.9 us with it.
+_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+FILE_FLAGS = {"elementwise.hip": _PRELOAD, "rope.hip": _PRELOAD}
 
 
 def _run(cmd, cwd=None, verbose=False):

@@ -136,6 +136,10 @@ namespace q3k
 
     // Sum over aligned groups of G consecutive lanes.  Every lane of a group
     // receives the bit-identical total (each step adds a commutative pair).
+    // Across 16-lane rows the partner value comes from v_permlane16_swap /
+    // v_permlane32_swap (VALU, no LDS round trip): after a swap of v with
+    // itself one result holds the even row (lower half) and the other the odd
+    // row (upper half), so their sum is the pair's total in every lane.
     template <int G>
     __device__ __forceinline__ float group_sum(float v)
     {
@@ -149,9 +153,15 @@ namespace q3k
         if constexpr (G >= 16)
             v += dpp_f<kDppMirror>(v);
         if constexpr (G >= 32)
-            v += __shfl_xor(v, 16, 64);
+        {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
         if constexpr (G >= 64)
-            v += __shfl_xor(v, 32, 64);
+        {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
         return v;
     }
 

@@ -58,11 +58,13 @@ namespace q3k
             const float *cache;
         };
 
-        // Position of a token: positions[t] or start + t % S; -1 when outside the table.
+        // Position of a token: positions[t] (POS: a positions array was
+        // given) or start + t % S; -1 when outside the table.
+        template <bool POS>
         __device__ __forceinline__ int64_t token_position(const RopeShape &rs, int64_t token)
         {
             int64_t pos;
-            if (rs.positions != nullptr)
+            if constexpr (POS)
                 pos = rs.positions[token];
             else
                 pos = rs.start + token % rs.seq;
@@ -71,10 +73,11 @@ namespace q3k
 
         // token_position for a per-lane token, in 32-bit arithmetic (tokens and
         // the sequence length are below 2^31)
+        template <bool POS>
         __device__ __forceinline__ int64_t lane_token_position(const RopeShape &rs, uint32_t token)
         {
             int64_t pos;
-            if (rs.positions != nullptr)
+            if constexpr (POS)
                 pos = rs.positions[token];
             else
             {
@@ -183,9 +186,18 @@ namespace q3k
         // pattern and the norm weights depend only on the lane and the
         // position, so they are loaded and unpacked once per wave.  With
         // COPY_V the wave also moves the matching V heads from vsrc to vdst.
-        template <bool NORM, int NTM, int HG, bool COPY_V, int PR>
+        //
+        // The position comes from `position()` (the token's table row, or -1
+        // when it is outside the table), called once the head loads are
+        // issued: the heads do not depend on it, so a position that has to be
+        // read from memory (decode) costs one round trip beside the head
+        // loads instead of one before them.  A position outside the table
+        // reads row 0 and the results are replaced by NaN, so no branch
+        // separates the loads.
+        template <bool NORM, int NTM, int HG, bool COPY_V, int PR, typename Position>
         __device__ __forceinline__ void rope_heads(const Vec8 *src, Vec8 *dst, const Vec8 *vsrc, Vec8 *vdst,
-                                                   const uint16_t *w, const float *table, int64_t pos, float eps)
+                                                   const uint16_t *w, const float *table, Position position,
+                                                   float eps)
         {
             const int lane16 = threadIdx.x % 16;
             Vec8 x[HG];
@@ -204,29 +216,24 @@ namespace q3k
             if constexpr (PR > 0)
                 __builtin_amdgcn_s_setprio(0);
 
-            if (pos < 0)
-            {
-                const Vec8 nan = {{kNanPair, kNanPair, kNanPair, kNanPair}};
-#pragma unroll
-                for (int i = 0; i < HG; ++i)
-                    store8<nt_store(NTM)>(dst + i * kHeadStride, nan);
-                if constexpr (COPY_V)
-                {
-#pragma unroll
-                    for (int i = 0; i < HG; ++i)
-                        store8<nt_store(NTM)>(vdst + i * kHeadStride, xv[i]);
-                }
-                return;
-            }
-
+            const int64_t pos = position();
+            const bool in_table = pos >= 0;
             float wf[8];
             if constexpr (NORM)
                 norm_weights(w, lane16, wf);
             float cs[8], sn[8];
-            table_row(table, pos, lane16, cs, sn);
+            table_row(table, in_table ? pos : 0, lane16, cs, sn);
+            const Vec8 nan = {{kNanPair, kNanPair, kNanPair, kNanPair}};
 #pragma unroll
             for (int i = 0; i < HG; ++i)
-                store8<nt_store(NTM)>(dst + i * kHeadStride, rotate_head<NORM>(x[i], wf, cs, sn, eps));
+            {
+                const Vec8 r = rotate_head<NORM>(x[i], wf, cs, sn, eps);
+                Vec8 out;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    out.d[j] = in_table ? r.d[j] : nan.d[j];
+                store8<nt_store(NTM)>(dst + i * kHeadStride, out);
+            }
             if constexpr (COPY_V)
             {
 #pragma unroll
@@ -243,7 +250,7 @@ namespace q3k
         }
 
         // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with
-        // HGK.  Q is rewritten in place; K in place too, or with KV into the
+        // HGK.  POS: positions come from rs.positions, else start + t % S.  Q is rewritten in place; K in place too, or with KV into the
         // cache rows given by `kv` (k itself is then only read).  Heads and
         // tokens are wave-uniform and below 2^31 (checked by the launcher).
         // ANYH bit 0 (Q) / bit 1 (K): that tensor's head count is not a
@@ -252,7 +259,7 @@ namespace q3k
         // rows, so the four rows of a wave may belong to different tokens
         // (token and position are per lane group), and the groups past the
         // last row of a partial last wave do nothing.
-        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, int ANYH>
+        template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, int ANYH, bool POS>
         __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
@@ -276,7 +283,7 @@ namespace q3k
                     // rows, tokens and the sequence length are below 2^31
                     // (checked by the launcher): 32-bit index arithmetic
                     const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(heads);
-                    const int64_t pos = lane_token_position(rs, token);
+                    const auto pos = [&]() __attribute__((always_inline)) { return lane_token_position<POS>(rs, token); };
                     const int64_t vec = row * kVecPerHead + threadIdx.x % 16;
                     if (is_q)
                     {
@@ -310,13 +317,13 @@ namespace q3k
                 const uint32_t head0 = static_cast<uint32_t>(wave * kHeadsPerWave * HGQ);
                 const uint32_t token = head0 / static_cast<uint32_t>(heads_q);
                 Vec8 *p = reinterpret_cast<Vec8 *>(q) + lane_vec(head0);
-                rope_heads<NORM, NTM, HGQ, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, token_position(rs, token),
-                                                  eps);
+                const auto pos = [&]() __attribute__((always_inline)) { return token_position<POS>(rs, token); };
+                rope_heads<NORM, NTM, HGQ, false, PR>(p, p, nullptr, nullptr, qw, rs.cache, pos, eps);
                 return;
             }
             const uint32_t head0 = static_cast<uint32_t>((wave - q_waves) * kHeadsPerWave * HGK);
             const uint32_t token = head0 / static_cast<uint32_t>(heads_k);
-            const int64_t pos = token_position(rs, token);
+            const auto pos = [&]() __attribute__((always_inline)) { return token_position<POS>(rs, token); };
             Vec8 *src = reinterpret_cast<Vec8 *>(k) + lane_vec(head0);
             if constexpr (KV)
             {
@@ -347,7 +354,8 @@ namespace q3k
                 const int64_t head_linear = idx / half;            // token * heads + head
                 const int64_t token = head_linear / heads;
                 uint16_t *head_ptr = x + head_linear * head_dim;
-                const int64_t pos = token_position(rs, token);
+                const int64_t pos =
+                    rs.positions != nullptr ? token_position<true>(rs, token) : token_position<false>(rs, token);
                 if (pos < 0)
                 {
                     head_ptr[pair] = 0x7fc0;
@@ -419,12 +427,20 @@ namespace q3k
             const int64_t q_waves = rope_waves(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : rope_waves(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            if (small)
-                rope_heads_kernel<NORM, ntm_small(NTM), HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
-                    <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            const dim3 grid(blocks), block(kBlock);
+            const bool pos = rs.positions != nullptr;
+            if (small && pos)
+                rope_heads_kernel<NORM, ntm_small(NTM), HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH, true>
+                    <<<grid, block, 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            else if (small)
+                rope_heads_kernel<NORM, ntm_small(NTM), HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH, false>
+                    <<<grid, block, 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+            else if (pos)
+                rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH, true>
+                    <<<grid, block, 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
             else
-                rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH>
-                    <<<dim3(blocks), dim3(kBlock), 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
+                rope_heads_kernel<NORM, NTM, HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH, false>
+                    <<<grid, block, 0, stream>>>(q, k, qw, kw, hq, hk, q_waves, total, rs, eps, kv);
         }
 
         // The instance the plan (plan_rope) names: heads per lane of Q and K, or
