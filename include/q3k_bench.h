@@ -29,9 +29,12 @@ Q3K_API int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3k_s
  * out1 = in0 + in1 word by word (in1 and out1 nullable; a missing in1 reads
  * as zero).  out0 may be in0 (in place).  The access pattern of a streaming op
  * at its size: silu_mul is (g, u) -> out, add + RMSNorm (h, d) -> (h, y), the
- * in-place RoPE q -> q.  bytes a multiple of 16, pointers 16-byte aligned. */
+ * in-place RoPE q -> q.  One 16-byte vector per thread, `threads` threads per
+ * block (64 .. 1024, a multiple of 64: the block size sets how finely the
+ * streams are spread over the XCDs, which moves the rate by several points).
+ * bytes a multiple of 16, pointers 16-byte aligned. */
 Q3K_API int q3k_bench_stream_u128(const void *in0, const void *in1, void *out0, void *out1, int64_t bytes,
-                                  q3k_stream_t stream);
+                                  int32_t threads, q3k_stream_t stream);
 
 /* Read ceiling of a strided row layout such as a KV-cache view: outer x inner
  * views, view (o, i) at base + o * outer_stride + i * inner_stride, each

@@ -102,7 +102,7 @@ _lib = None
 # name -> argtypes, in the order of include/q3k_bench.h (lib/libq3k_bench.so)
 BENCH_SIGNATURES = {
     "q3k_bench_copy_u128": [_p, _p, _i64, _p],
-    "q3k_bench_stream_u128": [_p, _p, _p, _p, _i64, _p],
+    "q3k_bench_stream_u128": [_p, _p, _p, _p, _i64, _i32, _p],
     "q3k_bench_read_rows_u128": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 _bench_lib = None
@@ -303,11 +303,12 @@ def bench_copy(src, dst, nbytes, stream=None):
     _check_bench(load_bench().q3k_bench_copy_u128(_ptr(src), _ptr(dst), nbytes, _ptr(stream)))
 
 
-def bench_stream(in0, in1, out0, out1, nbytes, stream=None):
-    """out0 = in0 XOR in1, out1 = in0 + in1 (in1, out1 may be None) with 128-bit loads and stores (q3k_bench.h)."""
+def bench_stream(in0, in1, out0, out1, nbytes, stream=None, threads=256):
+    """out0 = in0 XOR in1, out1 = in0 + in1 (in1, out1 may be None) with 128-bit loads and stores, `threads`
+    threads per block (q3k_bench.h)."""
     for buf, what in ((in0, "in0"), (in1, "in1"), (out0, "out0"), (out1, "out1")):
         _need(buf, nbytes, "bench_stream " + what)
-    _check_bench(load_bench().q3k_bench_stream_u128(_ptr(in0), _ptr(in1), _ptr(out0), _ptr(out1), nbytes,
+    _check_bench(load_bench().q3k_bench_stream_u128(_ptr(in0), _ptr(in1), _ptr(out0), _ptr(out1), nbytes, threads,
                                                     _ptr(stream)))
 
 

@@ -45,10 +45,10 @@ namespace q3k
         // stores of the streaming ops: out0 = in0 XOR in1, out1 = in0 + in1
         // (word-wise; in1 absent reads as zero).  In place when out0 is in0.
         // The HBM ceiling of an op's access pattern at its size.
-        __global__ __launch_bounds__(kBlock) void stream_vec_kernel(const Vec8 *in0, const Vec8 *in1, Vec8 *out0,
-                                                                    Vec8 *out1, int64_t nvec)
+        __global__ __launch_bounds__(1024) void stream_vec_kernel(const Vec8 *in0, const Vec8 *in1, Vec8 *out0,
+                                                                  Vec8 *out1, int64_t nvec)
         {
-            const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+            const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
             if (j >= nvec)
                 return;
             const Vec8 zero = {{0u, 0u, 0u, 0u}};
@@ -130,21 +130,23 @@ extern "C" int q3k_bench_copy_u128(const void *src, void *dst, int64_t bytes, q3
 }
 
 extern "C" int q3k_bench_stream_u128(const void *in0, const void *in1, void *out0, void *out1, int64_t bytes,
-                                     q3k_stream_t stream)
+                                     int32_t threads, q3k_stream_t stream)
 {
     using namespace q3k;
     if (bytes < 0 || bytes % 16 != 0)
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream size must be a non-negative multiple of 16 bytes");
+    if (threads < kWave || threads > 1024 || threads % kWave != 0)
+        return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream threads per block must be a multiple of 64 in [64, 1024]");
     if (bytes == 0)
         return Q3K_OK;
     if (in0 == nullptr || out0 == nullptr || !aligned16(in0) || !aligned16(out0) ||
         (in1 != nullptr && !aligned16(in1)) || (out1 != nullptr && !aligned16(out1)))
         return bench_error(Q3K_ERR_INVALID_ARGUMENT, "stream pointers must be 16-byte aligned (in0, out0 non-null)");
     const int64_t nvec = bytes / 16;
-    const int64_t blocks = (nvec + kBlock - 1) / kBlock;
-    if (!launch_fits(blocks, kBlock))
+    const int64_t blocks = blocks_for(nvec, threads);
+    if (!launch_fits(blocks, threads))
         return bench_error(Q3K_ERR_OVERFLOW, "stream size exceeds one launch");
-    stream_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+    stream_vec_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
         static_cast<const Vec8 *>(in0), static_cast<const Vec8 *>(in1), static_cast<Vec8 *>(out0),
         static_cast<Vec8 *>(out1), nvec);
     return bench_launch_status("bench_stream_u128");

@@ -44,7 +44,7 @@ namespace q3k
         if (!rope_heads_fit(tokens, hq) || (hk > 0 && !rope_heads_fit(tokens, hk)) || !rope_heads_fit(tokens, hq + hk))
             return false;
         const int64_t waves = rope_waves(tokens, hq, 1) + rope_waves(tokens, hk, 1);
-        return launch_fits(blocks_for(waves, kRopeWavesPerBlock), kBlock);
+        return launch_fits(blocks_for(waves, kRopeWavesPerBlock), kRopeBlock);
     }
 
     // hk = 0 for one tensor (q3k_rope_bf16).  aligned: every tensor, the table

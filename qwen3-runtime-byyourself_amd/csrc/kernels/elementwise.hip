@@ -21,11 +21,19 @@ namespace q3k
         constexpr int kUnrollSilu = 1;  // config 4, sustained: 79-80% of peak against 77% for 2 and 74% for 4
         constexpr int kNtmSilu = 3;
         constexpr int kPrioSilu = 1;  // wave priority while loads are issued
-        // XCD-contiguous tile remapping measured slower for both streams.
-        constexpr bool kRemapSilu = false;
-        constexpr bool kRemapAdd = false;
         constexpr int kUnrollAdd = 1;
         constexpr int kNtmAdd = 3;
+        // Blocks of the large launches: one wave (1 KiB of each stream per
+        // block), tiles in order.  Measured on MI355X for SwiGLU at 24-800 MB
+        // per stream (configs 4 and 5, their tensor-parallel-8 shard, and three
+        // sizes between): 64 threads gave 69.2-82.7% of peak HBM, the best or
+        // within 0.5 points of the best at every size; 256 threads gave
+        // 67.6-80.2% (config 4: 81.8% against 78.8%, config 5: 82.2% against
+        // 80.2%), 128 and 512-1024 threads in between.  Workgroups go to the
+        // eight XCDs in turn, so the block size sets how finely the streams
+        // are interleaved over the XCDs.  XCD-contiguous or XOR-permuted tile
+        // orders gained at some sizes and lost up to 5 points at others.
+        constexpr int kStreamBlock = 64;
 
         // exp(x) for the SiLU denominator: Cody-Waite style split of
         // x * log2(e) into an integer and a fraction, the fraction through the
@@ -150,16 +158,17 @@ namespace q3k
         }
 
         // OP 0: out = silu(a) * b.  OP 1: out = a + b (out == a for add_inplace).
-        // Each thread handles U vectors spaced one block apart.
-        template <int OP, int U, int NTM, int PR, bool REMAP>
-        __global__ __launch_bounds__(kBlock) void binary_vec_kernel(
+        // Blocks of BLOCK threads take tiles of BLOCK * U vectors; each thread
+        // handles U vectors spaced BLOCK apart.
+        template <int OP, int U, int NTM, int PR, int BLOCK>
+        __global__ __launch_bounds__(BLOCK) void binary_vec_kernel(
             const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t nvec, int64_t n)
         {
             const Vec8 *av = reinterpret_cast<const Vec8 *>(a);
             const Vec8 *bv = reinterpret_cast<const Vec8 *>(b);
             Vec8 *ov = reinterpret_cast<Vec8 *>(out);
-            const int64_t tile = tile_index<REMAP>(blockIdx.x, gridDim.x);
-            const int64_t base = tile * (kBlock * U) + threadIdx.x;
+            const int64_t tile = blockIdx.x;
+            const int64_t base = tile * (BLOCK * U) + threadIdx.x;
 
             Vec8 x[U], y[U];
             if constexpr (PR > 0)
@@ -167,7 +176,7 @@ namespace q3k
 #pragma unroll
             for (int i = 0; i < U; ++i)
             {
-                const int64_t j = base + static_cast<int64_t>(i) * kBlock;
+                const int64_t j = base + static_cast<int64_t>(i) * BLOCK;
                 if (j < nvec)
                 {
                     x[i] = load8<nt_load(NTM)>(av + j);
@@ -179,14 +188,14 @@ namespace q3k
 #pragma unroll
             for (int i = 0; i < U; ++i)
             {
-                const int64_t j = base + static_cast<int64_t>(i) * kBlock;
+                const int64_t j = base + static_cast<int64_t>(i) * BLOCK;
                 if (j < nvec)
                     store8<nt_store(NTM)>(ov + j, apply8<OP>(x[i], y[i]));
             }
 
             if (tile == 0)
             {
-                for (int64_t e = nvec * 8 + threadIdx.x; e < n; e += kBlock)
+                for (int64_t e = nvec * 8 + threadIdx.x; e < n; e += BLOCK)
                     out[e] = apply1<OP>(a[e], b[e]);
             }
         }
@@ -254,7 +263,6 @@ namespace q3k
             constexpr int U = OP == 0 ? kUnrollSilu : kUnrollAdd;
             constexpr int NTM = OP == 0 ? kNtmSilu : kNtmAdd;
             constexpr int PR = OP == 0 ? kPrioSilu : 0;
-            constexpr bool REMAP = OP == 0 ? kRemapSilu : kRemapAdd;
             const int64_t nvec = n / 8;
             const bool small = n * 2 <= kSmallLaunchBytes;
             if (OP == 0 && small && aligned_to(a, 8) && aligned_to(b, 8) && aligned_to(out, 8))
@@ -267,12 +275,13 @@ namespace q3k
             else if (small && aligned16(a) && aligned16(b) && aligned16(out))
             {
                 const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U)));
-                binary_vec_kernel<OP, U, ntm_small(NTM), PR, REMAP><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);
+                binary_vec_kernel<OP, U, ntm_small(NTM), PR, kBlock><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);
             }
-            else if (aligned16(a) && aligned16(b) && aligned16(out) && binary_vec_fits(n, U))
+            else if (aligned16(a) && aligned16(b) && aligned16(out) && binary_vec_fits(n, U, kStreamBlock))
             {
-                const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U)));
-                binary_vec_kernel<OP, U, NTM, PR, REMAP><<<grid, dim3(kBlock), 0, stream>>>(a, b, out, nvec, n);
+                const dim3 grid(static_cast<unsigned>(binary_vec_blocks(n, U, kStreamBlock)));
+                binary_vec_kernel<OP, U, NTM, PR, kStreamBlock>
+                    <<<grid, dim3(kStreamBlock), 0, stream>>>(a, b, out, nvec, n);
             }
             else
             {

@@ -17,7 +17,7 @@ namespace q3k
         constexpr int kNtm = 2;  // measured: plain loads (random rows), non-temporal stores
 
         template <int NTM>
-        __global__ __launch_bounds__(kBlock) void embedding_vec_kernel(
+        __global__ __launch_bounds__(kEmbeddingBlock) void embedding_vec_kernel(
             const int32_t *__restrict__ ids, int64_t tokens,
             const Vec8 *__restrict__ table, int64_t vocab, int64_t nvec,
             Vec8 *__restrict__ out)
@@ -93,7 +93,7 @@ extern "C" int q3k_embedding_bf16(const int32_t *ids, int64_t T, const uint16_t 
     if (H % 8 == 0 && aligned16(table) && aligned16(out) && embedding_vec_fits(T))
     {
         const dim3 grid(static_cast<unsigned>(blocks_for(T, kTokensPerBlock)));
-        embedding_vec_kernel<kNtm><<<grid, dim3(kBlock), 0, s>>>(
+        embedding_vec_kernel<kNtm><<<grid, dim3(kEmbeddingBlock), 0, s>>>(
             ids, T, reinterpret_cast<const Vec8 *>(table), V, H / 8, reinterpret_cast<Vec8 *>(out));
     }
     else

@@ -32,22 +32,32 @@ namespace q3k
 
     // Element-wise vector kernels: 8 elements a lane, `unroll` vectors a
     // lane, one block for an input of fewer than 8 elements.
-    inline int64_t binary_vec_blocks(int64_t n, int unroll)
+    inline int64_t binary_vec_blocks(int64_t n, int unroll, int block = kBlock)
     {
-        const int64_t blocks = blocks_for(n / 8, static_cast<int64_t>(kBlock) * unroll);
+        const int64_t blocks = blocks_for(n / 8, static_cast<int64_t>(block) * unroll);
         return blocks > 0 ? blocks : 1;
     }
-    inline bool binary_vec_fits(int64_t n, int unroll) { return launch_fits(binary_vec_blocks(n, unroll), kBlock); }
+    inline bool binary_vec_fits(int64_t n, int unroll, int block = kBlock)
+    {
+        return launch_fits(binary_vec_blocks(n, unroll, block), block);
+    }
 
-    // Embedding gather: one wave a token.
-    constexpr int kEmbeddingTokensPerBlock = kBlock / kWave;
+    // Embedding gather: one wave a token, kEmbeddingTokensPerBlock waves a block.
+    constexpr int kEmbeddingTokensPerBlock = 4;
+    constexpr int kEmbeddingBlock = kEmbeddingTokensPerBlock * kWave;
     inline bool embedding_vec_fits(int64_t tokens)
     {
-        return launch_fits(blocks_for(tokens, kEmbeddingTokensPerBlock), kBlock);
+        return launch_fits(blocks_for(tokens, kEmbeddingTokensPerBlock), kEmbeddingBlock);
     }
 
     // RMSNorm, several rows a block: groups of `group` lanes, one row each.
-    inline bool rms_rows_fit(int64_t rows, int group) { return launch_fits(blocks_for(rows, kBlock / group), kBlock); }
+    // Narrow RMSNorm rows: a group of `group` lanes a row, `block` lanes a
+    // block (kRmsRowsBlock unless a launch asks for more).
+    constexpr int kRmsRowsBlock = kWave;
+    inline bool rms_rows_fit(int64_t rows, int group, int block = kRmsRowsBlock)
+    {
+        return launch_fits(blocks_for(rows, block / group), block);
+    }
     // RMSNorm, one row a block of `waves` waves.
     inline bool rms_block_fits(int64_t rows, int waves) { return launch_fits(rows, static_cast<int64_t>(waves) * kWave); }
 
@@ -56,13 +66,14 @@ namespace q3k
     // most waves any head grouping launches.  The kernel also indexes rows
     // with 32-bit wave-uniform arithmetic, hence rows < 2^31.
     constexpr int kRopeHeadsPerWave = kWave / 16;
-    constexpr int kRopeWavesPerBlock = kBlock / kWave;
+    constexpr int kRopeWavesPerBlock = 4;
+    constexpr int kRopeBlock = kRopeWavesPerBlock * kWave;
     inline bool rope_heads_fit(int64_t tokens, int64_t heads)
     {
         if (tokens < 0 || heads <= 0 || tokens > (int64_t{1} << 31) / heads)
             return false;
         const int64_t rows = tokens * heads;
         return rows < (int64_t{1} << 31) &&
-               launch_fits(blocks_for(blocks_for(rows, kRopeHeadsPerWave), kRopeWavesPerBlock), kBlock);
+               launch_fits(blocks_for(blocks_for(rows, kRopeHeadsPerWave), kRopeWavesPerBlock), kRopeBlock);
     }
 } // namespace q3k

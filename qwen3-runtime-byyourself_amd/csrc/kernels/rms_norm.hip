@@ -138,19 +138,20 @@ namespace q3k
         }
 
         // Group of G lanes per row (G <= 64), VPT vectors per lane, RPG rows
-        // per lane group.  The rows of a wave are contiguous: lane group j of
-        // wave w takes rows w * (64 / G) * RPG + j + (64 / G) * r, r < RPG, so
-        // each load instruction covers 64 / G whole rows.  Every x load (of
-        // all RPG rows) is issued first, then d, then the weights once.
-        template <int G, int VPT, int RPG, int MODE, int NTM, bool FULL>
-        __global__ __launch_bounds__(kBlock) void rms_rows_kernel(
+        // per lane group, BLOCK lanes per block.  The rows of a wave are
+        // contiguous: lane group j of wave w takes rows
+        // w * (64 / G) * RPG + j + (64 / G) * r, r < RPG, so each load
+        // instruction covers 64 / G whole rows.  Every x load (of all RPG rows)
+        // is issued first, then d, then the weights once.
+        template <int G, int VPT, int RPG, int MODE, int NTM, bool FULL, int BLOCK>
+        __global__ __launch_bounds__(BLOCK) void rms_rows_kernel(
             uint16_t *__restrict__ h, const uint16_t *__restrict__ d,
             const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
             int64_t rows, int nvec, float inv_n, float eps, RowMap map)
         {
             constexpr int kGroups = kWave / G;
             const int lane = threadIdx.x % G;
-            const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+            const int64_t wave = static_cast<int64_t>(blockIdx.x) * (BLOCK / kWave) + threadIdx.x / kWave;
             const int64_t row0 = wave * kGroups * RPG + (threadIdx.x % kWave) / G;
             if (row0 >= rows)
                 return;
@@ -379,50 +380,54 @@ namespace q3k
         // stores with write-through (`sc1`) instead of streaming stores.
         inline bool small_launch(const Launch &l) { return l.rows * l.nvec * 16 <= kSmallLaunchBytes; }
 
-        template <int G, int VPT, int RPG, int MODE, int NTM>
+        template <int G, int VPT, int RPG, int MODE, int NTM, int BLOCK>
         void launch_rows_ntm(const Launch &l, const dim3 &grid)
         {
             if (l.nvec == G * VPT)
-                rms_rows_kernel<G, VPT, RPG, MODE, NTM, true><<<grid, dim3(kBlock), 0, l.stream>>>(
+                rms_rows_kernel<G, VPT, RPG, MODE, NTM, true, BLOCK><<<grid, dim3(BLOCK), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
             else
-                rms_rows_kernel<G, VPT, RPG, MODE, NTM, false><<<grid, dim3(kBlock), 0, l.stream>>>(
+                rms_rows_kernel<G, VPT, RPG, MODE, NTM, false, BLOCK><<<grid, dim3(BLOCK), 0, l.stream>>>(
                     l.h, l.d, l.w, l.y, l.rows, l.nvec, l.inv_n, l.eps, l.map);
         }
 
-        template <int G, int VPT, int RPG, int MODE>
+        template <int G, int VPT, int RPG, int MODE, int BLOCK = kRmsRowsBlock>
         bool launch_rows_rpg(const Launch &l)
         {
-            constexpr int kRowsPerBlock = kBlock / G * RPG;
-            if (!rms_rows_fit(l.rows, G))
+            constexpr int kRowsPerBlock = BLOCK / G * RPG;
+            if (!rms_rows_fit(l.rows, G, BLOCK))
                 return false;
             const dim3 grid(static_cast<unsigned>(blocks_for(l.rows, kRowsPerBlock)));
             if (small_launch(l))
-                launch_rows_ntm<G, VPT, RPG, MODE, ntm_small(ntm_rows<MODE>())>(l, grid);
+                launch_rows_ntm<G, VPT, RPG, MODE, ntm_small(ntm_rows<MODE>()), BLOCK>(l, grid);
             else
-                launch_rows_ntm<G, VPT, RPG, MODE, ntm_rows<MODE>()>(l, grid);
+                launch_rows_ntm<G, VPT, RPG, MODE, ntm_rows<MODE>(), BLOCK>(l, grid);
             return true;
         }
 
-        // Rows per lane group of the plain norm (measured on MI355X, nt loads,
-        // rotations past the Infinity Cache): 128-wide rows (the per-head Q/K
-        // norms) take four rows per 16-lane group for 16384 .. 65536 rows (the
-        // K norm of config 4, 65536 rows: 6.4 against 7.4 us with one) and one
-        // beyond (262144 rows: 22.2 against 23.2 us with four); 1024-wide rows
-        // take two per wave from 4096 rows (8192 rows: 6.4 against 7.4 us; 65536
-        // rows: equal).  Fewer rows (decode) keep one, for more waves.
+        // Rows per lane group and lanes per block of the plain norm (measured
+        // on MI355X, nt loads, rotations past the Infinity Cache).  One row per
+        // lane group in one-wave blocks by default: the per-head Q norm of
+        // config 4 (262144 128-wide rows) 20.8 against 21.6 us in four-wave
+        // blocks.  128-wide rows take four rows per 16-lane group in four-wave
+        // blocks for 16384 .. 65536 rows (the K norm of config 4, 65536 rows:
+        // 6.56 us, against 6.72-7.08 us for one, two, four or eight rows in
+        // one-wave blocks and 7.4 us for one row in four-wave blocks);
+        // 1024-wide rows take two per wave in four-wave blocks from 4096 rows
+        // (8192 rows: 6.4 against 7.4 us; 65536 rows: equal).  Fewer rows
+        // (decode) keep one, for more waves.
         template <int G, int VPT, int MODE>
         bool launch_rows(const Launch &l)
         {
             if constexpr (MODE == kNorm && G == 16 && VPT == 1)
             {
                 if (l.rows >= 16384 && l.rows <= 65536)
-                    return launch_rows_rpg<G, VPT, 4, MODE>(l);
+                    return launch_rows_rpg<G, VPT, 4, MODE, kBlock>(l);
             }
             if constexpr (MODE == kNorm && G == 64 && VPT == 2)
             {
                 if (l.rows >= 4096)
-                    return launch_rows_rpg<G, VPT, 2, MODE>(l);
+                    return launch_rows_rpg<G, VPT, 2, MODE, kBlock>(l);
             }
             return launch_rows_rpg<G, VPT, 1, MODE>(l);
         }

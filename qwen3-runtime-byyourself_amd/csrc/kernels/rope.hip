@@ -260,7 +260,7 @@ namespace q3k
         // (token and position are per lane group), and the groups past the
         // last row of a partial last wave do nothing.
         template <bool NORM, int NTM, int HGQ, int HGK, bool REMAP, bool KV, int PR, int ANYH, bool POS>
-        __global__ __launch_bounds__(kBlock) void rope_heads_kernel(
+        __global__ __launch_bounds__(kRopeBlock) void rope_heads_kernel(
             uint16_t *__restrict__ q, uint16_t *__restrict__ k,
             const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw,
             int32_t heads_q, int32_t heads_k, int64_t q_waves, int64_t total_waves,
@@ -427,7 +427,7 @@ namespace q3k
             const int64_t q_waves = rope_waves(tokens, hq, HGQ);
             const int64_t total = q_waves + (k == nullptr ? 0 : rope_waves(tokens, hk, HGK));
             const unsigned blocks = static_cast<unsigned>((total + kWavesPerBlock - 1) / kWavesPerBlock);
-            const dim3 grid(blocks), block(kBlock);
+            const dim3 grid(blocks), block(kRopeBlock);
             const bool pos = rs.positions != nullptr;
             if (small && pos)
                 rope_heads_kernel<NORM, ntm_small(NTM), HGQ, HGK, kRemapHeads, KV, kPrioHeads, ANYH, true>

@@ -35,7 +35,7 @@ namespace
                 "blocks_for rounding");
         require(blocks_for(big, 2) == big / 2 + 1 && blocks_for(big, 1) == big, "blocks_for overflows");
 
-        // element-wise: 8 elements a lane, 256 lanes a block, `unroll` vectors a lane
+        // element-wise: 8 elements a lane, 256 lanes a block (the default), `unroll` vectors a lane
         for (int unroll : {1, 2, 4})
         {
             const int64_t per_block = 8LL * 256 * unroll;
@@ -46,18 +46,33 @@ namespace
             require(!binary_vec_fits(last + 8, unroll), "element-wise grid past 2^32 work-items accepted");
             require(!binary_vec_fits(big, unroll), "huge element-wise input accepted");
         }
+        // the large launches' one-wave blocks: the same 2^32 work-item limit
+        {
+            const int64_t max64 = static_cast<int64_t>(UINT32_MAX) / 64;
+            const int64_t last = 8LL * 64 * max64;
+            require(binary_vec_blocks(last, 1, 64) == max64, "one-wave block count");
+            require(binary_vec_fits(last, 1, 64) && binary_vec_fits(last + 7, 1, 64), "largest one-wave grid rejected");
+            require(!binary_vec_fits(last + 8, 1, 64), "one-wave grid past 2^32 work-items accepted");
+            require(binary_vec_blocks(1, 1, 64) == 1, "short input: one one-wave block");
+        }
 
         // embedding: one wave a token
         require(kEmbeddingTokensPerBlock == 4, "embedding geometry");
         require(embedding_vec_fits(4 * kMax256) && !embedding_vec_fits(4 * kMax256 + 1), "embedding boundary");
         require(!embedding_vec_fits(big), "huge embedding accepted");
 
-        // RMSNorm: rows in lane groups, or one row a block of 1..8 waves
+        // RMSNorm: rows in lane groups (one-wave blocks by default, four-wave
+        // blocks where a launch asks for them), or one row a block of 1..8 waves
+        require(kRmsRowsBlock == 64, "rms rows geometry");
+        const int64_t max64 = kMaxItems / 64;
         for (int group : {1, 2, 4, 8, 16, 32, 64})
         {
-            const int64_t rows = static_cast<int64_t>(256 / group) * kMax256;
+            const int64_t rows = static_cast<int64_t>(64 / group) * max64;
             require(rms_rows_fit(rows, group) && !rms_rows_fit(rows + 1, group),
                     "rms rows boundary, group " + std::to_string(group));
+            const int64_t rows256 = static_cast<int64_t>(256 / group) * kMax256;
+            require(rms_rows_fit(rows256, group, 256) && !rms_rows_fit(rows256 + 1, group, 256),
+                    "rms rows boundary (four-wave blocks), group " + std::to_string(group));
         }
         for (int waves = 1; waves <= 8; ++waves)
         {

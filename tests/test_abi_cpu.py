@@ -83,6 +83,9 @@ def test_argument_errors_without_gpu(q3k):
     # grids past 2^32 - 1 work-items (256-thread blocks) are refused, not launched
     _expect(q3k.bench_copy, OverflowError, OV, fake, fake, 16 * 256 * (2**24))
     _expect(q3k.bench_stream, OverflowError, OV, fake, None, fake, None, 16 * 256 * (2**24))
+    _expect(q3k.bench_stream, OverflowError, OV, fake, None, fake, None, 16 * 64 * (2**26), None, 64)
+    for threads in (0, 32, 96, 2048):
+        _expect(q3k.bench_stream, ValueError, IA, fake, None, fake, None, 4096, None, threads)
     q3k.bench_copy(None, None, 0)   # nothing to move: no launch
     _expect(q3k.bench_read_rows, OverflowError, OV, fake, None, 2**13, 16, 2**11, 16, 1, 16, 16, fake)
 

@@ -747,12 +747,13 @@ def test_bench_read_rows(q3k, hip):
     check_exact("bench_read_rows sink", got, want)
 
 
+@pytest.mark.parametrize("threads", [64, 256, 1024])
 @pytest.mark.parametrize("n_in,n_out,in_place", [(2, 1, False), (2, 2, True), (1, 1, True), (1, 2, False)])
-def test_bench_stream(q3k, hip, n_in, n_out, in_place):
+def test_bench_stream(q3k, hip, n_in, n_out, in_place, threads):
     """The access-pattern ceiling aid reads its inputs and writes exactly its outputs: out0 = in0 XOR in1,
     out1 = in0 + in1 word for word (a missing in1 reads as zero), in place over in0 when asked, over a size that
-    leaves a partial last block, and nothing outside the buffers."""
-    announce(f"bench_stream in={n_in} out={n_out} in_place={in_place}")
+    leaves a partial last block at every block size, and nothing outside the buffers."""
+    announce(f"bench_stream in={n_in} out={n_out} in_place={in_place} threads={threads}")
     n = 16 * 1000 + 16 * 37          # bytes: 1037 vectors
     rng = np.random.default_rng(11)
     a = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
@@ -761,7 +762,7 @@ def test_bench_stream(q3k, hip, n_in, n_out, in_place):
     B = Guarded(hip, b) if n_in == 2 else None
     O0 = A if in_place else Guarded(hip, nbytes=n)
     O1 = Guarded(hip, nbytes=n) if n_out == 2 else None
-    q3k.bench_stream(A, B, O0, O1, n)
+    q3k.bench_stream(A, B, O0, O1, n, threads=threads)
     hip.synchronize()
     assert all(g.guards_intact() for g in (A, B, O0, O1) if g is not None)
     check_exact("bench_stream out0", O0.get(np.uint32, (n // 4,)), a ^ b)
