@@ -1,29 +1,34 @@
 // Embedding gather for gfx950: out[t, :] = table[ids[t], :], a zero row for
 // ids outside [0, V) (src/ops/embedding.cu:38-45).  Bit-exact copy.
 //
-// Fast path (H % 8 == 0, 16-byte aligned): one wave per token.  The id is
-// wave-uniform (scalar load); each lane moves VPT 128-bit vectors, all loads
-// issued before the stores, so a wave keeps VPT KiB of the row in flight.
-// Rows longer than 64 * VPT vectors are covered by a loop.  Other shapes
-// take a scalar kernel (one block per token, as the reference).
+// Fast path (H % 8 == 0, 16-byte aligned): WPT waves per token (one to
+// four, so that each wave moves about 2 KiB of a row per pass), four waves
+// per block.  The id is wave-uniform (scalar load); each lane moves kVpt
+// 128-bit vectors per pass, all loads issued before the stores; the waves of
+// a token interleave their passes over the row.  Measured on MI355X for
+// 8192 random rows of [151936, 4096]: four waves of 2 KiB per row 72.1% of
+// peak HBM, against 68.7% for one wave moving the whole 8 KiB row, 70.6%
+// for two waves of 4 KiB, 72.0% for eight waves of 1 KiB.  Other shapes take
+// a scalar kernel (one block per token, as the reference).
 #include "q3k_common.hpp"
 
 namespace q3k
 {
     namespace
     {
-        constexpr int kTokensPerBlock = kEmbeddingTokensPerBlock;
-        constexpr int kVpt = 8;
+        constexpr int kVpt = kEmbeddingVectorsPerLane;
         constexpr int kNtm = 2;  // measured: plain loads (random rows), non-temporal stores
 
-        template <int NTM>
+        template <int NTM, int WPT>
         __global__ __launch_bounds__(kEmbeddingBlock) void embedding_vec_kernel(
             const int32_t *__restrict__ ids, int64_t tokens,
             const Vec8 *__restrict__ table, int64_t vocab, int64_t nvec,
             Vec8 *__restrict__ out)
         {
             const int lane = threadIdx.x % kWave;
-            const int64_t token = static_cast<int64_t>(blockIdx.x) * kTokensPerBlock + threadIdx.x / kWave;
+            const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kEmbeddingBlock / kWave) + threadIdx.x / kWave;
+            const int64_t token = wave / WPT;
+            const int part = static_cast<int>(wave % WPT);
             if (token >= tokens)
                 return;
             const int32_t id = __builtin_amdgcn_readfirstlane(ids[token]);
@@ -31,12 +36,13 @@ namespace q3k
             if (id < 0 || static_cast<int64_t>(id) >= vocab)
             {
                 const Vec8 zero = {{0u, 0u, 0u, 0u}};
-                for (int64_t j = lane; j < nvec; j += kWave)
+                for (int64_t j = part * kWave + lane; j < nvec; j += WPT * kWave)
                     store8<nt_store(NTM)>(dst + j, zero);
                 return;
             }
             const Vec8 *src = table + static_cast<int64_t>(id) * nvec;
-            for (int64_t j0 = 0; j0 < nvec; j0 += static_cast<int64_t>(kWave) * kVpt)
+            for (int64_t j0 = static_cast<int64_t>(part) * kWave * kVpt; j0 < nvec;
+                 j0 += static_cast<int64_t>(WPT) * kWave * kVpt)
             {
                 Vec8 v[kVpt];
 #pragma unroll
@@ -90,11 +96,18 @@ extern "C" int q3k_embedding_bf16(const int32_t *ids, int64_t T, const uint16_t 
     if (V > INT64_MAX / H || T > INT64_MAX / H)
         return set_error(Q3K_ERR_OVERFLOW, "embedding size overflows");
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (H % 8 == 0 && aligned16(table) && aligned16(out) && embedding_vec_fits(T))
+    const int wpt = embedding_waves_per_token(H / 8);
+    if (H % 8 == 0 && aligned16(table) && aligned16(out) && embedding_vec_fits(T, wpt))
     {
-        const dim3 grid(static_cast<unsigned>(blocks_for(T, kTokensPerBlock)));
-        embedding_vec_kernel<kNtm><<<grid, dim3(kEmbeddingBlock), 0, s>>>(
-            ids, T, reinterpret_cast<const Vec8 *>(table), V, H / 8, reinterpret_cast<Vec8 *>(out));
+        const dim3 grid(static_cast<unsigned>(blocks_for(T * wpt, kEmbeddingBlock / kWave)));
+        const auto *tv = reinterpret_cast<const Vec8 *>(table);
+        auto *ov = reinterpret_cast<Vec8 *>(out);
+        if (wpt == 4)
+            embedding_vec_kernel<kNtm, 4><<<grid, dim3(kEmbeddingBlock), 0, s>>>(ids, T, tv, V, H / 8, ov);
+        else if (wpt == 2)
+            embedding_vec_kernel<kNtm, 2><<<grid, dim3(kEmbeddingBlock), 0, s>>>(ids, T, tv, V, H / 8, ov);
+        else
+            embedding_vec_kernel<kNtm, 1><<<grid, dim3(kEmbeddingBlock), 0, s>>>(ids, T, tv, V, H / 8, ov);
     }
     else
     {

@@ -42,12 +42,20 @@ namespace q3k
         return launch_fits(binary_vec_blocks(n, unroll, block), block);
     }
 
-    // Embedding gather: one wave a token, kEmbeddingTokensPerBlock waves a block.
-    constexpr int kEmbeddingTokensPerBlock = 4;
-    constexpr int kEmbeddingBlock = kEmbeddingTokensPerBlock * kWave;
-    inline bool embedding_vec_fits(int64_t tokens)
+    // Embedding gather: blocks of four waves, 1, 2 or 4 waves a token (rows
+    // of up to 128, 256 or more 128-bit vectors), kEmbeddingVectorsPerLane
+    // vectors a lane per pass over the row.
+    constexpr int kEmbeddingBlock = 4 * kWave;
+    constexpr int kEmbeddingVectorsPerLane = 2;
+    inline int embedding_waves_per_token(int64_t nvec)
     {
-        return launch_fits(blocks_for(tokens, kEmbeddingTokensPerBlock), kEmbeddingBlock);
+        const int64_t per_wave = static_cast<int64_t>(kWave) * kEmbeddingVectorsPerLane;
+        return nvec > 2 * per_wave ? 4 : nvec > per_wave ? 2 : 1;
+    }
+    inline bool embedding_vec_fits(int64_t tokens, int waves_per_token)
+    {
+        return tokens >= 0 && tokens <= INT64_MAX / 4 &&
+               launch_fits(blocks_for(tokens * waves_per_token, kEmbeddingBlock / kWave), kEmbeddingBlock);
     }
 
     // RMSNorm, several rows a block: groups of `group` lanes, one row each.

@@ -56,10 +56,19 @@ namespace
             require(binary_vec_blocks(1, 1, 64) == 1, "short input: one one-wave block");
         }
 
-        // embedding: one wave a token
-        require(kEmbeddingTokensPerBlock == 4, "embedding geometry");
-        require(embedding_vec_fits(4 * kMax256) && !embedding_vec_fits(4 * kMax256 + 1), "embedding boundary");
-        require(!embedding_vec_fits(big), "huge embedding accepted");
+        // embedding: 1, 2 or 4 waves a token in four-wave blocks
+        require(kEmbeddingBlock == 256 && kEmbeddingVectorsPerLane == 2, "embedding geometry");
+        require(embedding_waves_per_token(128) == 1 && embedding_waves_per_token(129) == 2 &&
+                    embedding_waves_per_token(256) == 2 && embedding_waves_per_token(257) == 4 &&
+                    embedding_waves_per_token(512) == 4 && embedding_waves_per_token(1) == 1,
+                "embedding waves per token");
+        for (int wpt : {1, 2, 4})
+        {
+            const int64_t tokens = 4 * kMax256 / wpt;
+            require(embedding_vec_fits(tokens, wpt) && !embedding_vec_fits(tokens + 1, wpt),
+                    "embedding boundary, waves per token " + std::to_string(wpt));
+            require(!embedding_vec_fits(big, wpt), "huge embedding accepted");
+        }
 
         // RMSNorm: rows in lane groups (one-wave blocks by default, four-wave
         // blocks where a launch asks for them), or one row a block of 1..8 waves
