@@ -18,8 +18,12 @@ namespace q3k
     constexpr int kBlock = 256;
 
     // A launch that writes at most this many bytes is small (a decode step):
-    // its kernels take their small-launch shapes and store policy.
-    constexpr int64_t kSmallLaunchBytes = int64_t{4} << 20;
+    // its kernels take their small-launch shapes and store policy.  Config 3's
+    // decode launches write 0.5-1.5 MB; config 2's (T = 512) Q/K norm + RoPE
+    // and SwiGLU write 3 MB and run faster in their large-launch shapes (the
+    // config-2 chain replayed from a HIP graph: 12.4 against 13.65 us per step
+    // with a 4 MiB bound; a 1 MiB bound slowed the decode step by 0.3 us).
+    constexpr int64_t kSmallLaunchBytes = int64_t{2} << 20;
 
     // Whether `blocks` blocks of `threads` threads fit one dispatch.
     inline bool launch_fits(int64_t blocks, int64_t threads)

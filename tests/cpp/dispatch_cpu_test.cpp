@@ -54,7 +54,10 @@ namespace
         const RopePlan c4 = plan_rope(8192, 32, 8, 128, true);
         require(c4.fast && c4.hg_q == 4 && c4.hg_k == 2 && c4.any_heads == 0, "config 4 instance");
         const RopePlan c3 = plan_rope(64, 32, 8, 128, true);
-        require(c3.fast && c3.hg_q == 1 && c3.hg_k == 1, "config 3 instance");
+        require(c3.fast && c3.small && c3.hg_q == 1 && c3.hg_k == 1, "config 3 instance");
+        // config 2 (0.6B prefill, 512 tokens, 16 + 8 heads: 3 MB written) takes the large-launch shapes
+        const RopePlan c2 = plan_rope(512, 16, 8, 128, true);
+        require(c2.fast && !c2.small && c2.hg_q == 4 && c2.hg_k == 2, "config 2 instance");
         // the generic kernels: head_dim 64, an unaligned tensor or table, rows past 2^31
         require(!plan_rope(8192, 32, 8, 64, true).fast, "head_dim 64 took the fast kernel");
         require(!plan_rope(8192, 32, 8, 128, false).fast, "unaligned tensors took the fast kernel");

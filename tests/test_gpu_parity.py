@@ -161,9 +161,10 @@ def test_elementwise_kat(q3k, hip, oracle):
 @pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (8, 0), (9, 0), (1000, 0), (8191, 0), (65536 + 3, 0),
                                       (1 << 20, 0), (4097, 2), (1 << 16, 2),
                                       # 8-byte aligned: the small-launch kernel's 64-bit accesses
-                                      (1001, 8), ((1 << 20) + 3, 8),
-                                      # above the small-launch size (4 MiB written): the 128-bit kernels
-                                      ((3 << 20) + 5, 0), ((3 << 20) + 1, 8)])
+                                      (1001, 8), ((1 << 19) + 3, 8),
+                                      # above the small-launch size (2 MiB written): the 128-bit kernels,
+                                      # or the scalar kernel for pointers that are not 16-byte aligned
+                                      ((1 << 20) + 3, 8), ((3 << 20) + 5, 0), ((3 << 20) + 1, 8)])
 def test_elementwise_shapes(q3k, hip, oracle, synth, n, offset):
     name = f"elementwise n={n} offset={offset}"
     announce(name)
