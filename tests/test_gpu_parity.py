@@ -207,7 +207,10 @@ def test_embedding_kat(q3k, hip, oracle):
     check_exact("embedding kat", run_embedding(q3k, hip, ids, table), oracle.embedding(ids, table))
 
 
+# one wave per token up to 128 vectors a row (H 1024), two up to 256 (H 1032, 2048), four beyond (H 4096,
+# 5120 with a partial second pass, 40960); H 12 and the 2-byte offset take the scalar kernel
 @pytest.mark.parametrize("V,H,T,offset", [(1000, 1024, 300, 0), (500, 4096, 77, 0), (300, 5120, 64, 0),
+                                          (200, 2048, 41, 0), (100, 1032, 7, 0),
                                           (50, 8, 9, 0), (64, 12, 33, 0), (100, 1024, 10, 2), (10, 40960, 3, 0)])
 def test_embedding_shapes(q3k, hip, oracle, synth, V, H, T, offset):
     name = f"embedding V={V} H={H} T={T} offset={offset}"
