@@ -250,7 +250,8 @@ namespace q3k
         }
 
         // Waves [0, q_waves) cover q with HGQ heads per lane, the rest k with
-        // HGK.  POS: positions come from rs.positions, else start + t % S.  Q is rewritten in place; K in place too, or with KV into the
+        // HGK.  POS: positions come from rs.positions, else start + t % S.
+        // Q is rewritten in place; K in place too, or with KV into the
         // cache rows given by `kv` (k itself is then only read).  Heads and
         // tokens are wave-uniform and below 2^31 (checked by the launcher).
         // ANYH bit 0 (Q) / bit 1 (K): that tensor's head count is not a
