@@ -256,16 +256,17 @@ def test_rope_shapes(q3k, hip, oracle, synth, B, S, heads, D, start, offset):
     check_band(oracle, name, run_rope(q3k, hip, x, B, S, heads, D, cache, start, offset=offset), prim, lo, hi)
 
 
-def test_rope_positions_overload(q3k, hip, oracle, synth):
-    announce("rope positions")
-    B, S, heads, D, P = 64, 1, 32, 128, 4096
+@pytest.mark.parametrize("B", [64, 2048])   # a small launch, and the large-launch instance with positions
+def test_rope_positions_overload(q3k, hip, oracle, synth, B):
+    announce(f"rope positions B={B}")
+    S, heads, D, P = 1, 32, 128, 4096
     cache = q3k.build_rope_cache(P, D, 1.0e6)
     x = synth.normal_bf16(111, 0, (B, S, heads * D))
     pos = synth.uniform_positions(111, 1, B * S, P)
     pos[:4] = [0, P - 1, P, -5]  # the last two are outside the table: NaN heads
     prim, lo, hi = oracle.rope(x, B, S, heads, D, cache, positions=pos)
     got = run_rope(q3k, hip, x, B, S, heads, D, cache, positions=pos)
-    check_band(oracle, "rope positions", got, prim, lo, hi)
+    check_band(oracle, f"rope positions B={B}", got, prim, lo, hi)
     assert np.all((got[2:4] & 0x7FFF) > 0x7F80)
 
 
@@ -411,22 +412,26 @@ def test_qk_norm_rope_special_values(q3k, hip, oracle, synth):
     check_band(oracle, "qk special k", gk, pk, lk, hk)
 
 
-def test_qk_norm_rope_positions_overload(q3k, hip, oracle, synth):
-    announce("qk_norm_rope positions")
-    B, S, Hq, Hkv, D, P = 64, 1, 32, 8, 128, 4096
+# 64 sequences: a decode-sized (small) launch, one head per lane group; 2048: the large-launch instance (4 query
+# heads per lane, 2 KV heads) with positions read from memory
+@pytest.mark.parametrize("B", [64, 2048])
+def test_qk_norm_rope_positions_overload(q3k, hip, oracle, synth, B):
+    announce(f"qk_norm_rope positions B={B}")
+    S, Hq, Hkv, D, P = 1, 32, 8, 128, 4096
     cache = q3k.build_rope_cache(P, D, 1.0e6)
     q = synth.normal_bf16(116, 0, (B, S, Hq * D))
     k = synth.normal_bf16(116, 1, (B, S, Hkv * D))
     qw = synth.normal_bf16(116, 2, (D,), mean=1.0, std=0.1)
     kw = synth.normal_bf16(116, 3, (D,), mean=1.0, std=0.1)
     pos = synth.uniform_positions(116, 4, B * S, P)
-    pos[5] = P + 10
+    pos[5], pos[B - 1] = P + 10, -3   # outside the table: NaN heads
     gq, gk = run_qknr(q3k, hip, q, k, qw, kw, B, S, Hq, Hkv, D, cache, positions=pos)
     pq, lq, hq = oracle.qk_norm_rope(q, qw, B, S, Hq, D, EPS, cache, positions=pos)
     pk, lk, hk = oracle.qk_norm_rope(k, kw, B, S, Hkv, D, EPS, cache, positions=pos)
-    check_band(oracle, "qknr positions q", gq, pq, lq, hq)
-    check_band(oracle, "qknr positions k", gk, pk, lk, hk)
-    assert np.all((gq[5] & 0x7FFF) > 0x7F80) and np.all((gk[5] & 0x7FFF) > 0x7F80)
+    check_band(oracle, f"qknr positions q B={B}", gq, pq, lq, hq)
+    check_band(oracle, f"qknr positions k B={B}", gk, pk, lk, hk)
+    for t in (5, B - 1):
+        assert np.all((gq[t] & 0x7FFF) > 0x7F80) and np.all((gk[t] & 0x7FFF) > 0x7F80)
 
 
 def test_fused_equals_unfused_on_gpu(q3k, hip, synth):
