@@ -530,6 +530,70 @@ def test_attention_row_subset_and_planted_mistake(oracle, synth):
     assert oracle.compare(wrong, full, lo, hi)["fail"] > 0
 
 
+@pytest.mark.parametrize("S", [512, 1024])
+def test_attention_band_separates_weight_roundings(oracle, synth, S):
+    """The band decides how many bits the matrix-core kernel must keep of each softmax weight p (the reference
+    multiplies fp32 p by v).  Emulated in float64 on sampled rows of the later half of the sequence (long key
+    ranges): p as a bf16 high part plus a bf16 remainder (the kernel's two P V products, ~16 bits) stays inside the
+    band everywhere; one bf16 rounding of p (8 bits) and one fp16 rounding (11 bits) are rejected."""
+    B, Hq, Hkv, D = 1, 8, 2, 128
+    G = Hq // Hkv
+    q = synth.normal_bf16(160, S, (B, S, Hq * D))
+    kc = synth.normal_bf16(161, S, (B, S, Hkv, D))
+    vc = synth.normal_bf16(162, S, (B, S, Hkv, D))
+    rng = np.random.default_rng(S)
+    rows = np.unique(np.concatenate([rng.integers(S * Hq // 2, S * Hq, 512), np.arange(S * Hq - Hq, S * Hq)]))
+    prim, lo, hi = oracle.gqa_attention(q, kc, vc, Hq, 0, rows=rows)
+
+    def bf16_rne(x):
+        return f32(synth.f32_to_bf16(np.asarray(x, np.float32)))
+
+    def e4m3_scaled(x):
+        """OCP fp8 e4m3 (3 mantissa bits, subnormal step 2^-9, max 448, ties to even) with a power-of-two scale
+        per 32 consecutive elements of the last axis (zero-padded to a multiple of 32), as block-scaled fp8 MFMA
+        operands carry it."""
+        n = x.shape[-1]
+        xp = np.zeros(x.shape[:-1] + (-(-n // 32) * 32,))
+        xp[..., :n] = x
+        xb = xp.reshape(x.shape[:-1] + (-1, 32))
+        m = np.abs(xb).max(axis=-1, keepdims=True)
+        scale = np.exp2(np.floor(np.log2(448.0 / np.where(m > 0, m, 448.0))))
+        a = np.abs(xb) * scale
+        step = np.exp2(np.maximum(np.floor(np.log2(np.where(a > 0, a, 1.0))), -6) - 3)
+        r = np.sign(xb) * np.minimum(np.round(a / step) * step, 448.0)
+        return (r / scale).reshape(xp.shape)[..., :n]
+
+    # e4m3 known values (block max 448, so scale 1): ties to even, the subnormal step, flush below half of it
+    kv = np.array([448.0, 1.0625, 1.1, 0.3, 2.0 ** -9, 1.5 * 2.0 ** -10, 2.0 ** -11, -3.3])
+    assert np.array_equal(e4m3_scaled(kv), [448.0, 1.0, 1.125, 0.3125, 2.0 ** -9, 2.0 ** -9, 0.0, -3.25])
+
+    qf = f32(q).astype(np.float64).reshape(S, Hq, D)
+    kf = f32(kc)[0].astype(np.float64)
+    vf = f32(vc)[0].astype(np.float64)
+    scale2 = np.float32(np.float32(1) / np.sqrt(np.float32(D))) * np.float32(1.4426950408889634)
+    outs = {"bf16 high + bf16 remainder": [], "fp16 high + fp8 remainder": [], "bf16": [], "fp16": []}
+    for r in rows:
+        s, h = divmod(int(r), Hq)
+        g = h // G
+        x = (kf[:s + 1, g] @ qf[s, h]).astype(np.float32) * scale2
+        p = np.exp2(x - x.max()).astype(np.float32)
+        l = p.astype(np.float64).sum()
+        ph = bf16_rne(p)
+        p16 = p.astype(np.float16).astype(np.float32)
+        v = vf[:s + 1, g]
+        sums = [(ph.astype(np.float64) + bf16_rne(p - ph)) @ v,
+                p16.astype(np.float64) @ v + e4m3_scaled((p - p16).astype(np.float64)) @ e4m3_scaled(v.T).T,
+                ph.astype(np.float64) @ v, p16.astype(np.float64) @ v]
+        for key, o in zip(outs, sums):
+            outs[key].append(synth.f32_to_bf16((o / l).astype(np.float32)))
+    fails = {key: oracle.compare(np.stack(o), prim, lo, hi)["fail"] for key, o in outs.items()}
+    n = rows.size * D
+    assert fails["bf16 high + bf16 remainder"] == 0, fails
+    assert fails["fp16 high + fp8 remainder"] == 0, fails
+    assert fails["bf16"] > 0.03 * n, fails
+    assert fails["fp16"] > 0, fails
+
+
 # ---------------------------------------------------------------- argmax
 
 def test_argmax_kat(oracle):
