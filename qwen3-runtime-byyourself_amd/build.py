@@ -13,6 +13,9 @@ Outputs (in-tree, git-ignored, shipped with the source tree to the GPU box):
 * ``bin/q3k_weight_io_bench``  the weight IO measurement (``bench/*.cpp``).
 * ``oracle/build/libq3k_oracle.so`` the CPU oracle (test infrastructure),
                                built through ``oracle/Makefile``.
+* ``oracle/_ref/*``           the reference's own test programs compiled
+                               against this library (``oracle/reference_programs.mk``),
+                               only where the reference's sources are present.
 
 Every call recompiles everything (``build()`` is the "does it build" check).
 """
@@ -151,6 +154,16 @@ def build_oracle(verbose=False) -> str:
     return os.path.join(ORACLE_DIR, "build", "libq3k_oracle.so")
 
 
+def build_reference_programs(verbose=False) -> str | None:
+    """The reference's own test programs against this library (``oracle/reference_programs.mk``), where the
+    reference's sources are present; None elsewhere."""
+    ref = os.environ.get("Q3K_REFERENCE_DIR", "/root/reference")
+    if not os.path.isdir(os.path.join(ref, "tests", "unit")):
+        return None
+    _run(["make", "-B", "-j8", "-C", ORACLE_DIR, "-f", "reference_programs.mk", f"REF={ref}"], verbose=verbose)
+    return os.path.join(ORACLE_DIR, "_ref")
+
+
 def build_cpp_tests(verbose=False) -> list[str]:
     sources = sorted(glob.glob(os.path.join(CPP_TEST_DIR, "*.cpp")))
     if not sources:
@@ -194,6 +207,7 @@ def build_all(verbose=False) -> dict:
               "oracle": build_oracle(verbose)}
     result["runtime"] = build_runtime(verbose)
     result["cpp_tests"] = build_cpp_tests(verbose) if result["runtime"] else []
+    result["reference_programs"] = build_reference_programs(verbose) if result["runtime"] else None
     result["benches"] = build_benches(verbose) if result["runtime"] else []
     return result
 

@@ -6,7 +6,8 @@
 // Strings are returned as UTF-8 (escapes decoded, surrogate pairs joined;
 // lone surrogates, raw control characters and ill-formed UTF-8 rejected).
 // A number reports whether it is an unsigned integer that fits 64 bits: no
-// sign, fraction or exponent ("-0", "1.0" and "1e3" are not).  Malformed
+// sign, fraction or exponent ("-0", "1.0" and "1e3" are not), and carries
+// its text for callers that need other readings of it.  Malformed
 // input throws std::runtime_error("JSON <reason> at byte <offset>").
 #pragma once
 
@@ -36,6 +37,9 @@ namespace qwen3::io_detail
         {
             bool is_unsigned = false;  // a non-negative integer below 2^64
             std::uint64_t value = 0;   // valid when is_unsigned
+            bool integral = false;     // no fraction and no exponent
+            bool negative = false;     // a leading minus sign
+            std::string_view text;     // the number as written (valid while the text is)
         };
 
         // A leading UTF-8 byte order mark (EF BB BF) is skipped, as nlohmann's
@@ -129,6 +133,7 @@ namespace qwen3::io_detail
         Number read_number()
         {
             skip_ws();
+            const std::size_t start = at_;
             Number n;
             bool negative = false, integral = true, fits = true;
             std::uint64_t v = 0;
@@ -175,6 +180,9 @@ namespace qwen3::io_detail
             }
             n.is_unsigned = !negative && integral && fits;
             n.value = n.is_unsigned ? v : 0;
+            n.integral = integral;
+            n.negative = negative;
+            n.text = text_.substr(start, at_ - start);
             return n;
         }
 

@@ -14,7 +14,8 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(REPO, "tests", "cpp", "build")
 CPU_TESTS = ["core_metadata_test", "tensor_view_test", "buffer_cpu_test", "tensor_cpu_test", "ops_validation_cpu_test",
              "io_cpu_test", "io_contract_cpu_test", "copy_crew_cpu_test",
-             "sample_finish_cpu_test", "launch_limits_cpu_test", "dispatch_cpu_test", "row_crew_cpu_test"]
+             "sample_finish_cpu_test", "launch_limits_cpu_test", "dispatch_cpu_test", "row_crew_cpu_test",
+             "model_config_cpu_test"]
 GPU_TESTS = ["buffer_gpu_test", "ops_gpu_test", "fused_gpu_test", "chain_oracle_gpu_test", "kv_cache_gpu_test",
              "sampling_gpu_test", "io_gpu_test", "decode_alloc_gpu_test"]
 
