@@ -61,9 +61,12 @@ namespace qwen3
 
         using Members = std::map<std::string, Member>;
 
+        // JSON numbers use '.' whatever LC_NUMERIC the process has set.
         double c_locale_strtod(const std::string &text)
         {
             static const locale_t c_locale = newlocale(LC_ALL_MASK, "C", static_cast<locale_t>(0));
+            if (c_locale == static_cast<locale_t>(0))
+                return std::strtod(text.c_str(), nullptr);
             return strtod_l(text.c_str(), nullptr, c_locale);
         }
 
